@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""Benchmark of the packed-affine GEMV hot path on one MI355X.
+
+Metric: Q4/g64 GEMV time and achieved HBM GB/s (fraction of
+the 8 TB/s peak) at 5120x17408 (the MLP down projection, rows x K) at B=1 and
+B=3; the 17408x5120 gate/up shape moves the same bytes and is reported too.
+
+A step is one launch of the metric kernel over one synthetic input batch
+(Q4/g64 codes, BF16 scales/biases, FP32 x), all resident in HBM before the
+timed region starts. Weights rotate over --copies distinct copies so that the
+50 MB matrix is not served from the 256 MB Infinity Cache.
+
+Timing: each launch is bracketed by two HIP events recorded on the library's
+stream; the per-launch duration is their difference, and `value` is the
+algorithmic bytes of one launch (codes + scales + biases + x + y) divided by
+the mean duration. The wall time of the whole timed region (synchronised on
+both sides) gives ms_per_step.
+
+The CPU baseline times the FP64 oracle (the reference's per-weight
+dequantise-then-accumulate closure, restated in C) on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "qwen-mlx-runner_amd"))
+
+import numpy as np  # noqa: E402
+
+import qmr  # noqa: E402
+import qmr.synth as synth  # noqa: E402
+
+METRIC = "Q4/g64 GEMV µs + achieved HBM GB/s (% peak), 5120x17408 at B=1 and B=3"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_kernel(gpu: qmr.Gpu, name: str, bufsets, params, steps: int, warmup: int):
+    """Per-launch event durations (ms) and the wall time of the timed region."""
+    _, threads = qmr.dispatch_layout(name, params)
+    cmd = gpu.begin()
+    for k in range(warmup):
+        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+    cmd.finish()
+    cmd.release()
+    cmd = gpu.begin()
+    marks = []
+    t0 = time.perf_counter()
+    for k in range(steps):
+        a = cmd.mark()
+        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+        b = cmd.mark()
+        marks.append((a, b))
+    cmd.finish()
+    wall = time.perf_counter() - t0
+    durs = [cmd.elapsed_ms(a, b) for a, b in marks]
+    cmd.release()
+    # Back-to-back launches without inner events: stream throughput.
+    cmd = gpu.begin()
+    a = cmd.mark()
+    for k in range(steps):
+        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+    b = cmd.mark()
+    cmd.finish()
+    stream_ms = cmd.elapsed_ms(a, b) / steps
+    cmd.release()
+    return durs, wall, stream_ms
+
+
+def cpu_baseline(m: synth.PackedMatrix, budget_s: float) -> dict:
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = max(1, min(cores, 16))
+    x = synth.activations(m.cols, 1, synth.DEFAULT_SEED, tag="bench")
+    run = lambda th, f: f(m.w, m.s, m.b, m.meta, x, m.rows, m.cols, m.bits, m.group, 1, th)
+    t = time.perf_counter()
+    run(threads, oracle.matmul_f64)
+    first = time.perf_counter() - t
+    reps = int(max(2, min(20, budget_s * 0.6 / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        run(threads, oracle.matmul_f64)
+        times.append(time.perf_counter() - t)
+    t = time.perf_counter()
+    run(1, oracle.matmul_f64)
+    single = time.perf_counter() - t
+    t = time.perf_counter()
+    run(threads, oracle.matmul_f32)
+    f32 = time.perf_counter() - t
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    med = statistics.median(times)
+    nbytes = synth.algorithmic_bytes(m, 1)
+    return {
+        "value": round(med * 1e6, 1), "unit": "us/matrix", "cores": threads, "kind": "port",
+        "sample": (f"FP64 oracle (oracle/qmr_oracle.c, per-weight dequantise then FP64 "
+                   f"accumulate) on the full {m.rows}x{m.cols} Q4/g64 BF16 B=1 matrix, "
+                   f"median of {reps} runs on {threads} threads"),
+        "gbps": round(nbytes / med / 1e9, 2),
+        "single_thread_us": round(single * 1e6, 1),
+        "fp32_accumulate_us": round(f32 * 1e6, 1),
+        "cpu_model": model, "host_cores_visible": cores,
+    }
+
+
+def load_traffic(tag: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+    p = ROOT / "profiles" / "pmc_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        d = json.loads(p.read_text())
+        return d.get(tag, {}).get("hbm_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-metric", action="store_true",
+                    help="time only the 5120x17408 shapes (for profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the hot path is "
+              f"single-GPU; multi-GPU sharding is design-only)", file=sys.stderr)
+        return 2
+    if int(os.environ.get("RANK", "0")) != 0:
+        return 0
+
+    gpu = qmr.Gpu("aligned")
+    log(f"bench: device {gpu.name()}, steps={args.steps} warmup={args.warmup} copies={args.copies}")
+    shapes = [("down", synth.MLP_SHAPES["down"])]
+    if not args.only_metric:
+        shapes.append(("gate_up", synth.MLP_SHAPES["gate_up"]))
+    results = []
+    metric_matrix = None
+    for tag, (rows, cols) in shapes:
+        m = synth.q4_bf16_matrix(rows, cols, synth.DEFAULT_SEED, tag=tag)
+        if tag == "down":
+            metric_matrix = m
+        mats = [(gpu.upload_bytes(m.w), gpu.upload_bytes(m.s), gpu.upload_bytes(m.b))
+                for _ in range(args.copies)]
+        for batch in (1, 3):
+            x = synth.activations(cols, batch, synth.DEFAULT_SEED, tag="bench")
+            xb = gpu.upload_f32(x.ravel())
+            ys = [gpu.alloc_f32(batch * rows) for _ in range(args.copies)]
+            bufsets = [[w, s, b, xb, y] for (w, s, b), y in zip(mats, ys)]
+            name = "matvec_affine_bf16" if batch == 1 else "matmul_affine_bf16"
+            params = [rows, cols, 4, 64] + ([batch] if batch > 1 else [])
+            log(f"bench: {tag} {rows}x{cols} B={batch} ({name})")
+            durs, wall, stream_ms = time_kernel(gpu, name, bufsets, params, args.steps, args.warmup)
+            nbytes = synth.algorithmic_bytes(m, batch)
+            mean_ms = statistics.fmean(durs)
+            med_ms = statistics.median(durs)
+            q = np.quantile(durs, [0.1, 0.9])
+            r = {
+                "shape": f"{rows}x{cols}", "tag": tag, "batch": batch, "kernel": gpu.last_kernel(),
+                "plan": list(gpu.gemv_plan(rows, cols, 4, batch)),
+                "us_mean": round(mean_ms * 1e3, 3), "us_median": round(med_ms * 1e3, 3),
+                "us_p10": round(q[0] * 1e3, 3), "us_p90": round(q[1] * 1e3, 3),
+                "us_stream": round(stream_ms * 1e3, 3),
+                "algorithmic_bytes": nbytes,
+                "gbps": round(nbytes / (mean_ms * 1e-3) / 1e9, 1),
+                "frac_peak": round(nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
+            }
+            log(f"bench:   {r['us_mean']} us mean ({r['us_median']} median, {r['us_stream']} "
+                f"back-to-back), {r['gbps']} GB/s = {100 * r['frac_peak']:.1f}% of peak")
+            results.append(r)
+            del bufsets, ys, xb
+        del mats
+
+    head = next(r for r in results if r["tag"] == "down" and r["batch"] == 1)
+    b3 = next(r for r in results if r["tag"] == "down" and r["batch"] == 3)
+    cpu = None
+    if not args.no_cpu and metric_matrix is not None:
+        log("bench: CPU baseline (FP64 oracle)")
+        cpu = cpu_baseline(metric_matrix, args.cpu_seconds)
+        log(f"bench:   CPU {cpu['value']} us/matrix on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": head["gbps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["wall_ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": "Q4/g64 BF16-metadata GEMV 5120x17408 (rows x K), B=1; B=3 block alongside",
+            "rows": 5120, "cols": 17408, "bits": 4, "group": 64, "metadata": "bf16",
+            "batch": 1, "rotating_weight_copies": args.copies,
+        },
+        "us_b1": head["us_mean"], "gbps_b1": head["gbps"], "frac_b1": head["frac_peak"],
+        "us_b3": b3["us_mean"], "gbps_b3": b3["gbps"], "frac_b3": b3["frac_peak"],
+        "roofline": {
+            "bound": "hbm",
+            "achieved": head["gbps"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": head["frac_peak"],
+            "traffic": load_traffic("down_b1"),
+            "kernel": head["kernel"],
+        },
+        "cpu_baseline": cpu,
+        "results": results,
+    }
+    print(json.dumps(line), flush=True)
+    gpu.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

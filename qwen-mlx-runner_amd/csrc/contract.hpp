@@ -1,0 +1,62 @@
+// Host-side dispatch contract: buffer-size layout, view checks, kernel
+// selection and mode parsing. Pure C++ (no HIP) so it is testable on a CPU.
+// Each function restates the reference's routine of the same name in
+// src/gpu.rs (cited per function in contract.cpp).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace qmr {
+
+// Error carrying the reference's message text; converted to a status code and
+// a thread-local message at the C-ABI boundary.
+struct Error {
+    int code;
+    std::string message;
+};
+
+enum class BlockMatmulMode : int { Legacy = 0, Shared = 1, MlpR2 = 2 };
+
+struct BlockKernelMode {
+    BlockMatmulMode matmul = BlockMatmulMode::Legacy;
+    bool batched_delta = true;
+};
+
+struct Layout {
+    std::vector<size_t> sizes;  // minimum byte size of each buffer view
+    size_t threads = 0;         // logical thread count of the reference ABI
+};
+
+// Metadata storage of a packed matrix on the device.
+enum class Meta : int { F32 = 0, BF16 = 1, F16 = 2 };
+
+// Throws Error on any violation, with the reference's message.
+Layout dispatch_layout(const std::string &name, const uint32_t *p, size_t n);
+void checked_buffer_range(size_t offset, size_t minimum, size_t length);
+bool ranges_overlap(size_t a, size_t a_len, size_t b, size_t b_len);
+
+const char *specialized_matvec(const uint32_t *p, bool aligned);
+const char *specialized_matvec_bf16(const uint32_t *p, bool aligned);
+const char *specialized_matmul(const std::string &name, const uint32_t *p, bool aligned,
+                               BlockMatmulMode mode);
+
+BlockKernelMode parse_block_kernel_mode(const char *matmul, const char *delta);
+BlockKernelMode parse_block_kernel_mode_for_device(const std::string &device_name,
+                                                   const char *matmul, const char *delta);
+
+bool supported_bf16_quantization(uint32_t bits, size_t group);
+bool pack_bf16_exact(const float *values, size_t n, uint16_t *out);
+
+// Name helpers.
+bool starts_with(const std::string &s, const char *prefix);
+bool ends_with(const std::string &s, const char *suffix);
+// Metadata storage implied by a reference (or added) kernel name.
+Meta meta_of_name(const std::string &name);
+bool is_affine_matrix_name(const std::string &name);  // matvec/matmul affine family
+bool is_block_name(const std::string &name);          // matmul_affine*, matmul_f16
+bool is_wide_name(const std::string &name);           // matmul_affine_wide*
+
+}  // namespace qmr

@@ -1,0 +1,60 @@
+// Launch interface between the host runtime (runtime.cpp) and the HIP
+// kernels (affine_gemv.hip, misc_kernels.hip, wide_mfma.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "contract.hpp"
+
+namespace qmr {
+
+// One packed-affine product: y[t][r] = sum_c (q*s + b) * x[t][c] for
+// t < batch (token-major x [batch][cols], y [batch][rows]).
+struct AffineArgs {
+    const uint32_t *w;  // [rows][cols*bits/32] packed codes, little-endian fields
+    const void *s;      // [rows][cols/group] metadata (F32 or 16-bit patterns)
+    const void *b;
+    const float *x;
+    float *y;
+    uint32_t rows, cols, bits, group, batch;
+    Meta meta;
+};
+
+// Tiling of the GEMV/block kernel. A workgroup has 8 half-wave row slots;
+// `ks` slots share a row group and split its K rounds, each slot owns `rr`
+// rows. rr/ks = 0 lets the planner choose.
+struct GemvPlan {
+    int rr = 0;
+    int ks = 0;
+};
+
+struct DeviceLimits {
+    size_t max_lds_per_block;  // bytes of LDS one workgroup may allocate
+    int num_cus;
+};
+
+// VALU GEMV / small-block kernel (batch 1..4, group 32/64/128, Q4/Q8).
+hipError_t launch_affine_gemv(const AffineArgs &a, GemvPlan plan, const DeviceLimits &lim,
+                              hipStream_t stream);
+// Reference-arithmetic kernel for any group size (also reference mode).
+hipError_t launch_affine_generic(const AffineArgs &a, hipStream_t stream);
+// Row dequantisation y[c] = q*s + b (bit-exact RN32).
+hipError_t launch_embed_affine(const uint32_t *w, const void *s, const void *b, Meta meta,
+                               uint32_t row, uint32_t cols, uint32_t bits, uint32_t group,
+                               float *y, hipStream_t stream);
+// Dense F16 weights: matvec / block and embedding row.
+hipError_t launch_dense_f16(const uint16_t *w, const float *x, float *y, uint32_t rows,
+                            uint32_t cols, uint32_t batch, hipStream_t stream);
+hipError_t launch_embed_f16(const uint16_t *w, uint32_t row, uint32_t cols, float *y,
+                            hipStream_t stream);
+// Wide block on MFMA (Q4/g64, batch up to 256).
+hipError_t launch_wide_mfma(const AffineArgs &a, const DeviceLimits &lim, hipStream_t stream);
+bool wide_mfma_supported(const AffineArgs &a);
+
+// The plan the GEMV launcher would use (for tests and tuning reports).
+GemvPlan plan_affine_gemv(const AffineArgs &a, GemvPlan forced, const DeviceLimits &lim);
+
+}  // namespace qmr

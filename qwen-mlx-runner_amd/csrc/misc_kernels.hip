@@ -1,0 +1,141 @@
+// The rest of the reference's matrix dispatch surface:
+//   - a reference-arithmetic affine GEMV/block for any group size (the
+//     reference's generic matvec_affine, kernels/qwen.metal:40-68, which its
+//     reference mode and unusual group sizes use);
+//   - row dequantisation (embed_affine[_bf16], kernels/qwen.metal:73-77,
+//     kernels/affine_bf16.metal:162-174), bit-exact RN32(q*s + b);
+//   - dense F16 matvec / blocks / embedding (kernels/qwen.metal:48-57,69-72,
+//     kernels/matmul_block.metal:213-248).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kernels.hpp"
+
+namespace qmr {
+namespace {
+
+__device__ __forceinline__ float meta_at(const void *p, size_t i, int meta) {
+    if (meta == 0) return static_cast<const float *>(p)[i];
+    const uint16_t h = static_cast<const uint16_t *>(p)[i];
+    if (meta == 1) return __uint_as_float(uint32_t(h) << 16);
+    return float(__builtin_bit_cast(_Float16, h));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over all 64 lanes; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x140>(v);
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// One wave per (row, rhs); lanes stride over columns. Per element the weight
+// is dequantised first, w = float(q)*s + b, then multiplied by x: the order
+// of the reference's affine() (kernels/qwen.metal:40-47).
+__global__ __launch_bounds__(256) void affine_generic_kernel(
+    const uint32_t *__restrict__ w, const void *__restrict__ s, const void *__restrict__ b,
+    int meta, const float *__restrict__ x, float *__restrict__ y, uint32_t rows, uint32_t cols,
+    uint32_t bits, uint32_t group, uint32_t batch) {
+    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63;
+    if (wave >= rows * batch) return;  // wave-uniform
+    const uint32_t row = wave % rows, t = wave / rows;
+    const uint32_t pack = 32 / bits, mask = (1u << bits) - 1u;
+    const uint32_t *wr = w + size_t(row) * (cols / pack);
+    const size_t gbase = size_t(row) * (cols / group);
+    const float *xt = x + size_t(t) * cols;
+    float v = 0.f;
+    for (uint32_t c = lane; c < cols; c += 64) {
+        const uint32_t q = (wr[c / pack] >> ((c % pack) * bits)) & mask;
+        const size_t gi = gbase + c / group;
+        const float wv = float(q) * meta_at(s, gi, meta) + meta_at(b, gi, meta);
+        v += wv * xt[c];
+    }
+    v = wave_sum(v);
+    if (lane == 0) y[size_t(t) * rows + row] = v;
+}
+
+// y[c] = RN32(q*s + b). q*s is exact in FP32 (q < 2^8, s with <= 24
+// significant bits), so the fused form equals the reference's mul-then-add.
+__global__ __launch_bounds__(256) void embed_affine_kernel(
+    const uint32_t *__restrict__ w, const void *__restrict__ s, const void *__restrict__ b,
+    int meta, uint32_t row, uint32_t cols, uint32_t bits, uint32_t group, float *__restrict__ y) {
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    const uint32_t pack = 32 / bits;
+    const uint32_t word = w[size_t(row) * (cols / pack) + c / pack];
+    const uint32_t q = (word >> ((c % pack) * bits)) & ((1u << bits) - 1u);
+    const size_t gi = size_t(row) * (cols / group) + c / group;
+    y[c] = __builtin_fmaf(float(q), meta_at(s, gi, meta), meta_at(b, gi, meta));
+}
+
+// Dense F16 weights times token-major FP32 x; one wave per (row, rhs).
+__global__ __launch_bounds__(256) void dense_f16_kernel(const uint16_t *__restrict__ w,
+                                                        const float *__restrict__ x,
+                                                        float *__restrict__ y, uint32_t rows,
+                                                        uint32_t cols, uint32_t batch) {
+    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63;
+    if (wave >= rows * batch) return;
+    const uint32_t row = wave % rows, t = wave / rows;
+    const uint16_t *wr = w + size_t(row) * cols;
+    const float *xt = x + size_t(t) * cols;
+    float v = 0.f;
+    for (uint32_t c = lane; c < cols; c += 64)
+        v = __builtin_fmaf(float(__builtin_bit_cast(_Float16, wr[c])), xt[c], v);
+    v = wave_sum(v);
+    if (lane == 0) y[size_t(t) * rows + row] = v;
+}
+
+__global__ __launch_bounds__(256) void embed_f16_kernel(const uint16_t *__restrict__ w,
+                                                        uint32_t row, uint32_t cols,
+                                                        float *__restrict__ y) {
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c < cols) y[c] = float(__builtin_bit_cast(_Float16, w[size_t(row) * cols + c]));
+}
+
+}  // namespace
+
+hipError_t launch_affine_generic(const AffineArgs &a, hipStream_t stream) {
+    const uint64_t waves = uint64_t(a.rows) * a.batch;
+    const uint64_t blocks = (waves * 64 + 255) / 256;
+    hipLaunchKernelGGL(affine_generic_kernel, dim3(uint32_t(blocks)), dim3(256), 0, stream, a.w,
+                       a.s, a.b, static_cast<int>(a.meta), a.x, a.y, a.rows, a.cols, a.bits,
+                       a.group, a.batch);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_affine(const uint32_t *w, const void *s, const void *b, Meta meta,
+                               uint32_t row, uint32_t cols, uint32_t bits, uint32_t group,
+                               float *y, hipStream_t stream) {
+    hipLaunchKernelGGL(embed_affine_kernel, dim3((cols + 255) / 256), dim3(256), 0, stream, w, s,
+                       b, static_cast<int>(meta), row, cols, bits, group, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_dense_f16(const uint16_t *w, const float *x, float *y, uint32_t rows,
+                            uint32_t cols, uint32_t batch, hipStream_t stream) {
+    const uint64_t waves = uint64_t(rows) * batch;
+    const uint64_t blocks = (waves * 64 + 255) / 256;
+    hipLaunchKernelGGL(dense_f16_kernel, dim3(uint32_t(blocks)), dim3(256), 0, stream, w, x, y,
+                       rows, cols, batch);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_f16(const uint16_t *w, uint32_t row, uint32_t cols, float *y,
+                            hipStream_t stream) {
+    hipLaunchKernelGGL(embed_f16_kernel, dim3((cols + 255) / 256), dim3(256), 0, stream, w, row,
+                       cols, y);
+    return hipGetLastError();
+}
+
+}  // namespace qmr

@@ -1,0 +1,638 @@
+// Host runtime behind include/qmr.h: device, buffers, commands and the
+// checked dispatch path. Replaces the reference's Metal backend object model
+// (Gpu / DispatchEncoder / command buffers, src/gpu.rs:95-876) with HIP:
+// one stream per device, asynchronous launches, one synchronisation per
+// command at qmr_command_finish.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <chrono>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/qmr.h"
+#include "contract.hpp"
+#include "kernels.hpp"
+
+using qmr::Error;
+
+struct qmr_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    std::string name;
+    std::string gemv_variant = "aligned";
+    bool reference = false;
+    bool bf16_metadata = false;
+    qmr::BlockKernelMode block_mode;
+    size_t max_alloc = 0;
+    qmr::DeviceLimits limits{};
+    size_t compacted_matrices = 0;
+    uint64_t metadata_saved_bytes = 0;
+    qmr::GemvPlan forced_plan;  // testing/tuning hook; {0,0} = planner
+    std::string last_kernel;    // selected reference pipeline label
+};
+
+struct qmr_buffer {
+    int ordinal = 0;
+    void *ptr = nullptr;
+    size_t length = 0;
+    std::atomic<int> refs{1};
+};
+
+struct qmr_command {
+    qmr_device *device = nullptr;
+    std::chrono::steady_clock::time_point started;
+    std::vector<hipEvent_t> marks;  // marks[0] = begin; finish appends the end
+    bool finished = false;
+    int end_mark = -1;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int set_error(int code, const std::string &message) {
+    g_error = message;
+    return code;
+}
+
+int hip_error(hipError_t e, const char *what) {
+    return set_error(QMR_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <typename F>
+int guarded(F &&f) {
+    try {
+        g_error.clear();
+        return f();
+    } catch (const Error &e) {
+        return set_error(e.code, e.message);
+    } catch (const std::exception &e) {
+        return set_error(QMR_ERR_INVALID, e.what());
+    }
+}
+
+void ensure(bool ok, const std::string &message, int code = QMR_ERR_INVALID) {
+    if (!ok) throw Error{code, message};
+}
+
+void check_hip(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw Error{QMR_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e)};
+}
+
+bool is_variant(const std::string &v) {
+    return v == "packed4" || v == "aligned" || v == "stream";
+}
+
+// Upper bound of threads a reference pipeline accepts per threadgroup: the
+// aligned/stream pipelines are built with 64, the other specialised matrix
+// pipelines with 128 (src/gpu.rs:394-414); generic ones keep the default.
+size_t pipeline_max_threads(const char *label) {
+    if (!label) return 1024;
+    std::string n = label;
+    if (qmr::ends_with(n, "_aligned") || qmr::ends_with(n, "_aligned_bf16") ||
+        qmr::ends_with(n, "_stream"))
+        return 64;
+    if (qmr::starts_with(n, "matvec_q") || qmr::starts_with(n, "matmul_")) return 128;
+    return 1024;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *qmr_last_error(void) { return g_error.c_str(); }
+
+int qmr_device_open(int ordinal, const qmr_device_options *options, qmr_device **out) {
+    return guarded([&]() -> int {
+        ensure(out != nullptr, "qmr_device_open: null output");
+        *out = nullptr;
+        qmr_device_options opt{};
+        if (options) opt = *options;
+        std::string variant = opt.gemv_variant ? opt.gemv_variant : "aligned";
+        ensure(is_variant(variant), "QWEN_METAL_GEMV must be packed4, aligned or stream");
+        std::string metadata = opt.metadata_mode ? opt.metadata_mode : "f32";
+        ensure(metadata == "f32" || metadata == "bf16", "QWEN_METAL_METADATA must be f32 or bf16");
+        int count = 0;
+        hipError_t e = hipGetDeviceCount(&count);
+        ensure(e == hipSuccess && count > 0,
+               "No HIP GPU available; this backend requires an AMD Instinct GPU (gfx950)",
+               QMR_ERR_DEVICE);
+        ensure(ordinal >= 0 && ordinal < count, "GPU ordinal out of range", QMR_ERR_INVALID);
+        hipDeviceProp_t prop;
+        check_hip(hipGetDeviceProperties(&prop, ordinal), "hipGetDeviceProperties");
+        std::string arch = prop.gcnArchName;
+        ensure(arch.rfind("gfx950", 0) == 0,
+               "Kernels are built for gfx950 (MI355X); device reports " + arch, QMR_ERR_DEVICE);
+        auto *dev = new qmr_device();
+        dev->ordinal = ordinal;
+        dev->name = prop.name;
+        dev->gemv_variant = variant;
+        dev->reference = opt.reference != 0;
+        dev->bf16_metadata = metadata == "bf16" && !dev->reference;
+        try {
+            dev->block_mode =
+                qmr::parse_block_kernel_mode_for_device(dev->name, opt.block_matmul, opt.block_delta);
+        } catch (...) {
+            delete dev;
+            throw;
+        }
+        dev->max_alloc = prop.totalGlobalMem;
+        dev->limits.max_lds_per_block = prop.sharedMemPerBlock;
+        dev->limits.num_cus = prop.multiProcessorCount;
+        e = hipSetDevice(ordinal);
+        if (e == hipSuccess) e = hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            delete dev;
+            check_hip(e, "hipStreamCreate");
+        }
+        *out = dev;
+        return QMR_OK;
+    });
+}
+
+void qmr_device_close(qmr_device *device) {
+    if (!device) return;
+    hipSetDevice(device->ordinal);
+    if (device->stream) {
+        hipStreamSynchronize(device->stream);
+        hipStreamDestroy(device->stream);
+    }
+    delete device;
+}
+
+const char *qmr_device_name(const qmr_device *device) { return device ? device->name.c_str() : ""; }
+
+const char *qmr_kernel_mode(const qmr_device *device) {
+    if (!device) return "";
+    return device->reference ? "reference" : device->gemv_variant.c_str();
+}
+
+const char *qmr_metadata_mode(const qmr_device *device) {
+    return device && device->bf16_metadata ? "bf16" : "f32";
+}
+
+void qmr_block_kernel_mode(const qmr_device *device, int *matmul, int *batched_delta) {
+    if (!device) return;
+    if (matmul) *matmul = static_cast<int>(device->block_mode.matmul);
+    if (batched_delta) *batched_delta = device->block_mode.batched_delta ? 1 : 0;
+}
+
+int qmr_set_block_kernel_mode(qmr_device *device, int matmul, int batched_delta) {
+    return guarded([&]() -> int {
+        ensure(device != nullptr, "null device");
+        ensure(matmul >= 0 && matmul <= 2, "invalid block matmul mode");
+        device->block_mode.matmul = static_cast<qmr::BlockMatmulMode>(matmul);
+        device->block_mode.batched_delta = batched_delta != 0;
+        return QMR_OK;
+    });
+}
+
+int qmr_compact_metadata(const qmr_device *device, uint32_t bits, size_t group,
+                         const float *scales, const float *biases, size_t n, uint16_t *s_out,
+                         uint16_t *b_out) {
+    if (!device || !device->bf16_metadata || !qmr::supported_bf16_quantization(bits, group))
+        return 0;
+    if (!qmr::pack_bf16_exact(scales, n, s_out)) return 0;
+    if (!qmr::pack_bf16_exact(biases, n, b_out)) return 0;
+    return 1;
+}
+
+void qmr_record_compacted_metadata(qmr_device *device, uint64_t saved_bytes) {
+    if (!device) return;
+    device->compacted_matrices += 1;
+    device->metadata_saved_bytes += saved_bytes;
+}
+
+void qmr_metadata_stats(const qmr_device *device, size_t *matrices, uint64_t *saved_bytes) {
+    if (!device) return;
+    if (matrices) *matrices = device->compacted_matrices;
+    if (saved_bytes) *saved_bytes = device->metadata_saved_bytes;
+}
+
+// ---- buffers ----
+
+int qmr_buffer_alloc(qmr_device *device, size_t bytes, qmr_buffer **out) {
+    return guarded([&]() -> int {
+        ensure(device && out, "qmr_buffer_alloc: null argument");
+        *out = nullptr;
+        const size_t n = bytes < 4 ? 4 : bytes;
+        ensure(n <= device->max_alloc, "GPU allocation " + std::to_string(n) +
+                                           " exceeds device buffer limit " +
+                                           std::to_string(device->max_alloc));
+        check_hip(hipSetDevice(device->ordinal), "hipSetDevice");
+        void *p = nullptr;
+        check_hip(hipMalloc(&p, n), "hipMalloc");
+        hipError_t e = hipMemset(p, 0, n);
+        if (e != hipSuccess) {
+            hipFree(p);
+            check_hip(e, "hipMemset");
+        }
+        auto *b = new qmr_buffer();
+        b->ordinal = device->ordinal;
+        b->ptr = p;
+        b->length = n;
+        *out = b;
+        return QMR_OK;
+    });
+}
+
+int qmr_buffer_upload(qmr_device *device, const void *data, size_t bytes, qmr_buffer **out) {
+    return guarded([&]() -> int {
+        ensure(device && out, "qmr_buffer_upload: null argument");
+        *out = nullptr;
+        if (bytes == 0) return qmr_buffer_alloc(device, 0, out);
+        ensure(data != nullptr, "qmr_buffer_upload: null data");
+        ensure(bytes <= device->max_alloc, "GPU allocation " + std::to_string(bytes) +
+                                               " exceeds device buffer limit " +
+                                               std::to_string(device->max_alloc));
+        check_hip(hipSetDevice(device->ordinal), "hipSetDevice");
+        void *p = nullptr;
+        check_hip(hipMalloc(&p, bytes), "hipMalloc");
+        hipError_t e = hipMemcpy(p, data, bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            hipFree(p);
+            check_hip(e, "hipMemcpy");
+        }
+        auto *b = new qmr_buffer();
+        b->ordinal = device->ordinal;
+        b->ptr = p;
+        b->length = bytes;
+        *out = b;
+        return QMR_OK;
+    });
+}
+
+int qmr_buffer_read(const qmr_buffer *buffer, size_t offset, void *dst, size_t bytes) {
+    return guarded([&]() -> int {
+        ensure(buffer && (dst || bytes == 0), "qmr_buffer_read: null argument");
+        size_t end;
+        ensure(!__builtin_add_overflow(offset, bytes, &end) && end <= buffer->length,
+               "Read exceeds GPU buffer");
+        if (bytes == 0) return QMR_OK;
+        check_hip(hipSetDevice(buffer->ordinal), "hipSetDevice");
+        check_hip(hipMemcpy(dst, static_cast<const char *>(buffer->ptr) + offset, bytes,
+                            hipMemcpyDeviceToHost),
+                  "hipMemcpy");
+        return QMR_OK;
+    });
+}
+
+int qmr_buffer_write(qmr_buffer *buffer, size_t offset, const void *src, size_t bytes) {
+    return guarded([&]() -> int {
+        ensure(buffer && (src || bytes == 0), "qmr_buffer_write: null argument");
+        size_t end;
+        ensure(!__builtin_add_overflow(offset, bytes, &end) && end <= buffer->length,
+               "Write exceeds GPU buffer");
+        if (bytes == 0) return QMR_OK;
+        check_hip(hipSetDevice(buffer->ordinal), "hipSetDevice");
+        check_hip(hipMemcpy(static_cast<char *>(buffer->ptr) + offset, src, bytes,
+                            hipMemcpyHostToDevice),
+                  "hipMemcpy");
+        return QMR_OK;
+    });
+}
+
+size_t qmr_buffer_length(const qmr_buffer *buffer) { return buffer ? buffer->length : 0; }
+
+void qmr_buffer_retain(qmr_buffer *buffer) {
+    if (buffer) buffer->refs.fetch_add(1);
+}
+
+void qmr_buffer_release(qmr_buffer *buffer) {
+    if (!buffer) return;
+    if (buffer->refs.fetch_sub(1) == 1) {
+        hipSetDevice(buffer->ordinal);
+        hipFree(buffer->ptr);
+        delete buffer;
+    }
+}
+
+// ---- commands ----
+
+int qmr_command_begin(qmr_device *device, qmr_command **out) {
+    return guarded([&]() -> int {
+        ensure(device && out, "qmr_command_begin: null argument");
+        *out = nullptr;
+        check_hip(hipSetDevice(device->ordinal), "hipSetDevice");
+        auto *cmd = new qmr_command();
+        cmd->device = device;
+        cmd->started = std::chrono::steady_clock::now();
+        hipEvent_t ev;
+        hipError_t e = hipEventCreate(&ev);
+        if (e == hipSuccess) e = hipEventRecord(ev, device->stream);
+        if (e != hipSuccess) {
+            delete cmd;
+            check_hip(e, "hipEventRecord");
+        }
+        cmd->marks.push_back(ev);
+        *out = cmd;
+        return QMR_OK;
+    });
+}
+
+int qmr_command_mark(qmr_command *command, int *index) {
+    return guarded([&]() -> int {
+        ensure(command && !command->finished, "qmr_command_mark: command not open");
+        hipEvent_t ev;
+        check_hip(hipEventCreate(&ev), "hipEventCreate");
+        hipError_t e = hipEventRecord(ev, command->device->stream);
+        if (e != hipSuccess) {
+            hipEventDestroy(ev);
+            check_hip(e, "hipEventRecord");
+        }
+        command->marks.push_back(ev);
+        if (index) *index = int(command->marks.size()) - 1;
+        return QMR_OK;
+    });
+}
+
+int qmr_command_finish(qmr_command *command, qmr_frame_timing *timing) {
+    return guarded([&]() -> int {
+        ensure(command && !command->finished, "qmr_command_finish: command not open");
+        using clock = std::chrono::steady_clock;
+        const double encode = std::chrono::duration<double>(clock::now() - command->started).count();
+        const auto commit_start = clock::now();
+        hipEvent_t end;
+        check_hip(hipEventCreate(&end), "hipEventCreate");
+        hipError_t e = hipEventRecord(end, command->device->stream);
+        if (e != hipSuccess) {
+            hipEventDestroy(end);
+            check_hip(e, "hipEventRecord");
+        }
+        command->marks.push_back(end);
+        command->end_mark = int(command->marks.size()) - 1;
+        const double commit = std::chrono::duration<double>(clock::now() - commit_start).count();
+        const auto wait_start = clock::now();
+        e = hipEventSynchronize(end);
+        const double wait = std::chrono::duration<double>(clock::now() - wait_start).count();
+        command->finished = true;
+        if (e == hipSuccess) e = hipGetLastError();
+        check_hip(e, "GPU command failed");
+        float ms = 0.f;
+        check_hip(hipEventElapsedTime(&ms, command->marks[0], end), "hipEventElapsedTime");
+        if (timing) {
+            timing->cpu_encode_seconds = encode;
+            timing->cpu_commit_seconds = commit;
+            timing->gpu_seconds = double(ms) * 1e-3;
+            timing->completion_wait_seconds = wait;
+        }
+        return QMR_OK;
+    });
+}
+
+int qmr_command_elapsed(const qmr_command *command, int from, int to, double *ms) {
+    return guarded([&]() -> int {
+        ensure(command && command->finished, "qmr_command_elapsed: command not finished");
+        ensure(from >= 0 && to >= 0 && size_t(from) < command->marks.size() &&
+                   size_t(to) < command->marks.size(),
+               "qmr_command_elapsed: unknown mark");
+        float v = 0.f;
+        check_hip(hipEventElapsedTime(&v, command->marks[from], command->marks[to]),
+                  "hipEventElapsedTime");
+        if (ms) *ms = v;
+        return QMR_OK;
+    });
+}
+
+void qmr_command_release(qmr_command *command) {
+    if (!command) return;
+    if (!command->finished) hipStreamSynchronize(command->device->stream);
+    for (hipEvent_t ev : command->marks) hipEventDestroy(ev);
+    delete command;
+}
+
+// ---- encode: the checked dispatch path of Gpu::encode_inner
+// (src/gpu.rs:628-848): layout, buffer views, aliasing, mode bans,
+// selection, thread and group checks, then the launch. ----
+
+int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffers,
+               const size_t *offsets, size_t nbuffers, const uint32_t *params, size_t nparams,
+               size_t threads, size_t group_size) {
+    return guarded([&]() -> int {
+        ensure(command && !command->finished, "qmr_encode: command not open");
+        ensure(cname != nullptr, "qmr_encode: null kernel name");
+        qmr_device *dev = command->device;
+        const std::string name = cname;
+        ensure(params != nullptr || nparams == 0, "qmr_encode: null params");
+        const qmr::Layout layout = qmr::dispatch_layout(name, params, nparams);
+        ensure(!dev->reference || !qmr::starts_with(name, "matmul_"),
+               "Block matrix dispatch is unavailable in reference mode");
+        ensure(layout.sizes.size() == nbuffers, name + ": expected " +
+                                                    std::to_string(layout.sizes.size()) +
+                                                    " buffers, got " + std::to_string(nbuffers));
+        auto off = [&](size_t i) -> size_t { return offsets ? offsets[i] : 0; };
+        for (size_t i = 0; i < nbuffers; ++i) {
+            ensure(buffers[i] != nullptr, name + ": buffer " + std::to_string(i) + " is null");
+            ensure(buffers[i]->ordinal == dev->ordinal,
+                   name + ": buffer " + std::to_string(i) + " belongs to another device");
+            try {
+                qmr::checked_buffer_range(off(i), layout.sizes[i], buffers[i]->length);
+            } catch (const Error &e) {
+                throw Error{e.code, name + ": buffer " + std::to_string(i) + ": " + e.message};
+            }
+        }
+        // A matrix-block output is never an input (src/gpu.rs:658-672).
+        if (qmr::starts_with(name, "matmul_")) {
+            const size_t out = nbuffers - 1;
+            for (size_t i = 0; i < out; ++i) {
+                if (buffers[i] == buffers[out]) {
+                    ensure(!qmr::ranges_overlap(off(i), layout.sizes[i], off(out), layout.sizes[out]),
+                           name + ": output overlaps input buffer " + std::to_string(i));
+                }
+            }
+        }
+        const qmr::Meta meta = qmr::meta_of_name(name);
+        // src/gpu.rs:688-691.
+        ensure(!dev->reference || !qmr::ends_with(name, "_bf16"),
+               "BF16 metadata dispatch is unavailable in reference mode");
+        ensure(!dev->reference || meta != qmr::Meta::F16,
+               "F16 metadata dispatch is unavailable in reference mode");
+
+        // Selection: the reference pipeline the Metal backend would pick
+        // (src/gpu.rs:692-760). It decides the thread-group contract and is
+        // recorded for inspection; the HIP instance is chosen below.
+        const char *label = nullptr;
+        const bool aligned_variant = dev->gemv_variant == "aligned";
+        const bool wide = qmr::is_wide_name(name);
+        if (qmr::starts_with(name, "matmul_") && !wide && meta != qmr::Meta::F16) {
+            label = qmr::specialized_matmul(
+                name, params,
+                aligned_variant && off(0) % 8 == 0 && off(name == "matmul_f16" ? 1 : 3) % 16 == 0,
+                dev->block_mode.matmul);
+            ensure(label != nullptr, "Unsupported matrix block specialization", QMR_ERR_UNSUPPORTED);
+        } else if (name == "matvec_affine_bf16") {
+            ensure(off(3) % 16 == 0, "BF16 matvec input requires a 16-byte aligned offset");
+            label = qmr::specialized_matvec_bf16(params, aligned_variant && off(0) % 8 == 0);
+            ensure(label != nullptr, "Unsupported BF16 affine quantization", QMR_ERR_UNSUPPORTED);
+        } else if (!dev->reference && name == "matvec_affine" && off(3) % 16 == 0) {
+            if (dev->gemv_variant == "stream" && off(0) % 8 == 0 && params[2] == 4 &&
+                uint64_t(params[0]) * params[1] <= uint64_t(INT32_MAX)) {
+                if (params[3] == 32) label = "matvec_q4_g32_stream";
+                if (params[3] == 64) label = "matvec_q4_g64_stream";
+                if (params[3] == 128) label = "matvec_q4_g128_stream";
+            }
+            if (!label) label = qmr::specialized_matvec(params, aligned_variant && off(0) % 8 == 0);
+        }
+        ensure(threads == layout.threads, name + ": expected " + std::to_string(layout.threads) +
+                                              " threads, got " + std::to_string(threads));
+        const size_t actual_group =
+            (label && (qmr::ends_with(label, "_aligned") || qmr::ends_with(label, "_aligned_bf16") ||
+                       qmr::ends_with(label, "_stream")))
+                ? 64
+                : group_size;
+        ensure(group_size >= 32 && group_size % 32 == 0 && actual_group <= pipeline_max_threads(label),
+               name + ": invalid threadgroup size " + std::to_string(group_size));
+
+        dev->last_kernel = label ? label : name;
+        check_hip(hipSetDevice(dev->ordinal), "hipSetDevice");
+        auto ptr = [&](size_t i) -> char * {
+            return static_cast<char *>(buffers[i]->ptr) + off(i);
+        };
+        hipError_t e = hipSuccess;
+        if (qmr::starts_with(name, "embed_affine")) {
+            e = qmr::launch_embed_affine(reinterpret_cast<const uint32_t *>(ptr(0)), ptr(1), ptr(2),
+                                         meta, params[0], params[1], params[2], params[3],
+                                         reinterpret_cast<float *>(ptr(3)), dev->stream);
+        } else if (name == "embed_f16") {
+            e = qmr::launch_embed_f16(reinterpret_cast<const uint16_t *>(ptr(0)), params[0],
+                                      params[1], reinterpret_cast<float *>(ptr(1)), dev->stream);
+        } else if (name == "matvec_f16" || name == "matmul_f16") {
+            const uint32_t batch = name == "matmul_f16" ? params[2] : 1;
+            e = qmr::launch_dense_f16(reinterpret_cast<const uint16_t *>(ptr(0)),
+                                      reinterpret_cast<const float *>(ptr(1)),
+                                      reinterpret_cast<float *>(ptr(2)), params[0], params[1],
+                                      batch, dev->stream);
+        } else {
+            qmr::AffineArgs a;
+            a.w = reinterpret_cast<const uint32_t *>(ptr(0));
+            a.s = ptr(1);
+            a.b = ptr(2);
+            a.x = reinterpret_cast<const float *>(ptr(3));
+            a.y = reinterpret_cast<float *>(ptr(4));
+            a.rows = params[0];
+            a.cols = params[1];
+            a.bits = params[2];
+            a.group = params[3];
+            a.batch = qmr::starts_with(name, "matmul_") ? params[4] : 1;
+            a.meta = meta;
+            const bool fast_group = a.group == 32 || a.group == 64 || a.group == 128;
+            if (wide && qmr::wide_mfma_supported(a)) {
+                e = qmr::launch_wide_mfma(a, dev->limits, dev->stream);
+            } else if (wide) {
+                // Wide blocks outside the MFMA kernel's format run as
+                // successive small blocks of up to four RHS.
+                for (uint32_t t0 = 0; t0 < a.batch && e == hipSuccess; t0 += 4) {
+                    qmr::AffineArgs sub = a;
+                    sub.batch = a.batch - t0 < 4 ? a.batch - t0 : 4;
+                    sub.x = a.x + size_t(t0) * a.cols;
+                    sub.y = a.y + size_t(t0) * a.rows;
+                    e = qmr::launch_affine_gemv(sub, dev->forced_plan, dev->limits, dev->stream);
+                }
+            } else if (dev->reference || !fast_group) {
+                e = qmr::launch_affine_generic(a, dev->stream);
+            } else {
+                e = qmr::launch_affine_gemv(a, dev->forced_plan, dev->limits, dev->stream);
+            }
+        }
+        check_hip(e, "kernel launch");
+        return QMR_OK;
+    });
+}
+
+// ---- host-only contract functions ----
+
+int qmr_dispatch_layout(const char *name, const uint32_t *params, size_t nparams, size_t *sizes,
+                        size_t max_sizes, size_t *nsizes, size_t *threads) {
+    return guarded([&]() -> int {
+        ensure(name != nullptr, "null kernel name");
+        const qmr::Layout l = qmr::dispatch_layout(name, params, nparams);
+        ensure(l.sizes.size() <= max_sizes, "size array too small");
+        for (size_t i = 0; i < l.sizes.size(); ++i) sizes[i] = l.sizes[i];
+        if (nsizes) *nsizes = l.sizes.size();
+        if (threads) *threads = l.threads;
+        return QMR_OK;
+    });
+}
+
+int qmr_checked_buffer_range(size_t offset, size_t minimum, size_t length) {
+    return guarded([&]() -> int {
+        qmr::checked_buffer_range(offset, minimum, length);
+        return QMR_OK;
+    });
+}
+
+int qmr_ranges_overlap(size_t a, size_t a_len, size_t b, size_t b_len) {
+    return qmr::ranges_overlap(a, a_len, b, b_len) ? 1 : 0;
+}
+
+const char *qmr_specialized_matvec(const uint32_t *params, int aligned, int bf16) {
+    return bf16 ? qmr::specialized_matvec_bf16(params, aligned != 0)
+                : qmr::specialized_matvec(params, aligned != 0);
+}
+
+const char *qmr_specialized_matmul(const char *name, const uint32_t *params, size_t nparams,
+                                   int aligned, int mode) {
+    if (!name || !params) return nullptr;
+    const std::string n = name;
+    if ((n == "matmul_f16" && nparams != 3) || (n != "matmul_f16" && nparams != 5)) return nullptr;
+    return qmr::specialized_matmul(n, params, aligned != 0, static_cast<qmr::BlockMatmulMode>(mode));
+}
+
+int qmr_parse_block_kernel_mode(const char *device_name, const char *matmul, const char *delta,
+                                int *matmul_out, int *batched_delta_out) {
+    return guarded([&]() -> int {
+        const qmr::BlockKernelMode m = qmr::parse_block_kernel_mode_for_device(
+            device_name ? device_name : "", matmul, delta);
+        if (matmul_out) *matmul_out = static_cast<int>(m.matmul);
+        if (batched_delta_out) *batched_delta_out = m.batched_delta ? 1 : 0;
+        return QMR_OK;
+    });
+}
+
+int qmr_pack_bf16_exact(const float *values, size_t n, uint16_t *out) {
+    return qmr::pack_bf16_exact(values, n, out) ? 1 : 0;
+}
+
+int qmr_supported_bf16_quantization(uint32_t bits, size_t group) {
+    return qmr::supported_bf16_quantization(bits, group) ? 1 : 0;
+}
+
+// ---- testing / tuning hooks (declared in include/qmr_tuning.h) ----
+
+int qmr_set_gemv_plan(qmr_device *device, int rr, int ks) {
+    return guarded([&]() -> int {
+        ensure(device != nullptr, "null device");
+        device->forced_plan.rr = rr;
+        device->forced_plan.ks = ks;
+        return QMR_OK;
+    });
+}
+
+const char *qmr_last_kernel(const qmr_device *device) {
+    return device ? device->last_kernel.c_str() : "";
+}
+
+int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32_t bits,
+                  uint32_t batch, int *rr, int *ks) {
+    return guarded([&]() -> int {
+        ensure(device != nullptr, "null device");
+        qmr::AffineArgs a{};
+        a.rows = rows;
+        a.cols = cols;
+        a.bits = bits;
+        a.group = 64;
+        a.batch = batch;
+        const qmr::GemvPlan p = qmr::plan_affine_gemv(a, device->forced_plan, device->limits);
+        if (rr) *rr = p.rr;
+        if (ks) *ks = p.ks;
+        return QMR_OK;
+    });
+}
+
+size_t qmr_device_max_lds(const qmr_device *device) {
+    return device ? device->limits.max_lds_per_block : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,417 @@
+"""Python binding of libqmr_hip.so (include/qmr.h) through ctypes.
+
+It mirrors the reference engine's Metal backend interface (`Gpu`,
+`DispatchEncoder`, src/gpu.rs:95-876) so that tests and benchmarks read like
+the reference's own: a `Gpu` uploads buffers, `begin()` opens a command,
+`encode(...)` checks and enqueues one dispatch by reference kernel name and
+`finish()` synchronises and returns the frame timing.
+
+The library is built by qwen-mlx-runner_amd/build.py. Loading fails loudly if
+it is missing: there is no CPU fallback behind this interface.
+"""
+from __future__ import annotations
+
+import atexit
+import ctypes as C
+import os
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent.parent
+LIB_PATH = PKG_DIR / "libqmr_hip.so"
+
+QMR_OK = 0
+QMR_ERR_INVALID = 1
+QMR_ERR_DEVICE = 2
+QMR_ERR_UNSUPPORTED = 3
+
+BLOCK_MODES = {"legacy": 0, "shared": 1, "mlp-r2": 2}
+BLOCK_MODE_NAMES = {v: k for k, v in BLOCK_MODES.items()}
+
+EXPORTED_SYMBOLS = (
+    "qmr_last_error", "qmr_device_open", "qmr_device_close", "qmr_device_name",
+    "qmr_kernel_mode", "qmr_metadata_mode", "qmr_block_kernel_mode",
+    "qmr_set_block_kernel_mode", "qmr_compact_metadata", "qmr_record_compacted_metadata",
+    "qmr_metadata_stats", "qmr_buffer_alloc", "qmr_buffer_upload", "qmr_buffer_read",
+    "qmr_buffer_write", "qmr_buffer_length", "qmr_buffer_retain", "qmr_buffer_release",
+    "qmr_command_begin", "qmr_encode", "qmr_command_mark", "qmr_command_finish",
+    "qmr_command_elapsed", "qmr_command_release", "qmr_dispatch_layout",
+    "qmr_checked_buffer_range", "qmr_ranges_overlap", "qmr_specialized_matvec",
+    "qmr_specialized_matmul", "qmr_parse_block_kernel_mode", "qmr_pack_bf16_exact",
+    "qmr_supported_bf16_quantization", "qmr_set_gemv_plan", "qmr_gemv_plan",
+    "qmr_last_kernel", "qmr_device_max_lds",
+)
+
+
+class QmrError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+class _Options(C.Structure):
+    _fields_ = [("gemv_variant", C.c_char_p), ("metadata_mode", C.c_char_p),
+                ("block_matmul", C.c_char_p), ("block_delta", C.c_char_p),
+                ("reference", C.c_int)]
+
+
+class _Timing(C.Structure):
+    _fields_ = [("cpu_encode_seconds", C.c_double), ("cpu_commit_seconds", C.c_double),
+                ("gpu_seconds", C.c_double), ("completion_wait_seconds", C.c_double)]
+
+
+@dataclass
+class FrameTiming:
+    """FrameTiming of src/gpu/timing.rs:8-21."""
+    cpu_encode_seconds: float
+    cpu_commit_seconds: float
+    gpu_seconds: float
+    completion_wait_seconds: float
+
+
+_lib: Optional[C.CDLL] = None
+_alive = True  # cleared at interpreter exit: no handle is released after that
+
+
+def _at_exit() -> None:
+    global _alive
+    _alive = False
+
+
+atexit.register(_at_exit)
+
+
+def lib() -> C.CDLL:
+    """Load libqmr_hip.so once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("QMR_LIB", LIB_PATH))
+    if not path.exists():
+        raise ImportError(f"{path} is missing: build it with python qwen-mlx-runner_amd/build.py")
+    L = C.CDLL(str(path))
+    vp, sz, u32p, szp = C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32), C.POINTER(C.c_size_t)
+    sig = {
+        "qmr_last_error": (C.c_char_p, []),
+        "qmr_device_open": (C.c_int, [C.c_int, C.POINTER(_Options), C.POINTER(vp)]),
+        "qmr_device_close": (None, [vp]),
+        "qmr_device_name": (C.c_char_p, [vp]),
+        "qmr_kernel_mode": (C.c_char_p, [vp]),
+        "qmr_metadata_mode": (C.c_char_p, [vp]),
+        "qmr_block_kernel_mode": (None, [vp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "qmr_set_block_kernel_mode": (C.c_int, [vp, C.c_int, C.c_int]),
+        "qmr_compact_metadata": (C.c_int, [vp, C.c_uint32, sz, vp, vp, sz, vp, vp]),
+        "qmr_record_compacted_metadata": (None, [vp, C.c_uint64]),
+        "qmr_metadata_stats": (None, [vp, szp, C.POINTER(C.c_uint64)]),
+        "qmr_buffer_alloc": (C.c_int, [vp, sz, C.POINTER(vp)]),
+        "qmr_buffer_upload": (C.c_int, [vp, vp, sz, C.POINTER(vp)]),
+        "qmr_buffer_read": (C.c_int, [vp, sz, vp, sz]),
+        "qmr_buffer_write": (C.c_int, [vp, sz, vp, sz]),
+        "qmr_buffer_length": (sz, [vp]),
+        "qmr_buffer_retain": (None, [vp]),
+        "qmr_buffer_release": (None, [vp]),
+        "qmr_command_begin": (C.c_int, [vp, C.POINTER(vp)]),
+        "qmr_encode": (C.c_int, [vp, C.c_char_p, C.POINTER(vp), szp, sz, u32p, sz, sz, sz]),
+        "qmr_command_mark": (C.c_int, [vp, C.POINTER(C.c_int)]),
+        "qmr_command_finish": (C.c_int, [vp, C.POINTER(_Timing)]),
+        "qmr_command_elapsed": (C.c_int, [vp, C.c_int, C.c_int, C.POINTER(C.c_double)]),
+        "qmr_command_release": (None, [vp]),
+        "qmr_dispatch_layout": (C.c_int, [C.c_char_p, u32p, sz, szp, sz, szp, szp]),
+        "qmr_checked_buffer_range": (C.c_int, [sz, sz, sz]),
+        "qmr_ranges_overlap": (C.c_int, [sz, sz, sz, sz]),
+        "qmr_specialized_matvec": (C.c_char_p, [u32p, C.c_int, C.c_int]),
+        "qmr_specialized_matmul": (C.c_char_p, [C.c_char_p, u32p, sz, C.c_int, C.c_int]),
+        "qmr_parse_block_kernel_mode": (C.c_int, [C.c_char_p, C.c_char_p, C.c_char_p,
+                                                  C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "qmr_pack_bf16_exact": (C.c_int, [vp, sz, vp]),
+        "qmr_supported_bf16_quantization": (C.c_int, [C.c_uint32, sz]),
+        "qmr_set_gemv_plan": (C.c_int, [vp, C.c_int, C.c_int]),
+        "qmr_gemv_plan": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                    C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "qmr_last_kernel": (C.c_char_p, [vp]),
+        "qmr_device_max_lds": (sz, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(code: int) -> None:
+    if code != QMR_OK:
+        raise QmrError(code, lib().qmr_last_error().decode())
+
+
+def _u32(params: Sequence[int]):
+    arr = (C.c_uint32 * max(len(params), 1))(*[int(p) & 0xFFFFFFFF for p in params])
+    return arr
+
+
+def _s(v: Optional[str]) -> Optional[bytes]:
+    return None if v is None else v.encode()
+
+
+# ---- host-only contract (no GPU needed) ----
+
+def dispatch_layout(name: str, params: Sequence[int]) -> tuple[list[int], int]:
+    """dispatch_layout (src/gpu.rs:1041-1294) for the matrix kernels."""
+    sizes = (C.c_size_t * 8)()
+    n = C.c_size_t()
+    threads = C.c_size_t()
+    _check(lib().qmr_dispatch_layout(name.encode(), _u32(params), len(params), sizes, 8,
+                                     C.byref(n), C.byref(threads)))
+    return [sizes[i] for i in range(n.value)], threads.value
+
+
+def checked_buffer_range(offset: int, minimum: int, length: int) -> None:
+    _check(lib().qmr_checked_buffer_range(offset, minimum, length))
+
+
+def ranges_overlap(a: int, a_len: int, b: int, b_len: int) -> bool:
+    return bool(lib().qmr_ranges_overlap(a, a_len, b, b_len))
+
+
+def specialized_matvec(params: Sequence[int], aligned: bool, bf16: bool = False) -> Optional[str]:
+    r = lib().qmr_specialized_matvec(_u32(params), int(aligned), int(bf16))
+    return None if r is None else r.decode()
+
+
+def specialized_matmul(name: str, params: Sequence[int], aligned: bool,
+                       mode: str = "legacy") -> Optional[str]:
+    r = lib().qmr_specialized_matmul(name.encode(), _u32(params), len(params), int(aligned),
+                                     BLOCK_MODES[mode])
+    return None if r is None else r.decode()
+
+
+def parse_block_kernel_mode(device_name: str, matmul: Optional[str] = None,
+                            delta: Optional[str] = None) -> tuple[str, bool]:
+    m, d = C.c_int(), C.c_int()
+    _check(lib().qmr_parse_block_kernel_mode(device_name.encode(), _s(matmul), _s(delta),
+                                             C.byref(m), C.byref(d)))
+    return BLOCK_MODE_NAMES[m.value], bool(d.value)
+
+
+def pack_bf16_exact(values: np.ndarray) -> Optional[np.ndarray]:
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(v.size, dtype=np.uint16)
+    ok = lib().qmr_pack_bf16_exact(v.ctypes.data, v.size, out.ctypes.data)
+    return out if ok else None
+
+
+def supported_bf16_quantization(bits: int, group: int) -> bool:
+    return bool(lib().qmr_supported_bf16_quantization(bits, group))
+
+
+# ---- device objects ----
+
+class Buffer:
+    """A refcounted device buffer (a Metal buffer handle in the reference)."""
+
+    def __init__(self, handle: int):
+        self._h = C.c_void_p(handle)
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def __len__(self) -> int:
+        return int(lib().qmr_buffer_length(self._h))
+
+    def read(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        _check(lib().qmr_buffer_read(self._h, offset, out.ctypes.data, out.nbytes))
+        return out
+
+    def read_bytes(self, offset: int = 0, nbytes: Optional[int] = None) -> bytes:
+        n = len(self) - offset if nbytes is None else nbytes
+        out = np.empty(n, dtype=np.uint8)
+        _check(lib().qmr_buffer_read(self._h, offset, out.ctypes.data, n))
+        return out.tobytes()
+
+    def write(self, data: np.ndarray, offset: int = 0) -> None:
+        d = np.ascontiguousarray(data)
+        _check(lib().qmr_buffer_write(self._h, offset, d.ctypes.data, d.nbytes))
+
+    def release(self) -> None:
+        if self._h:
+            lib().qmr_buffer_release(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        if _alive:
+            try:
+                self.release()
+            except Exception:
+                pass
+
+
+class Command:
+    """One command: dispatches enqueued on the device stream, then finish()."""
+
+    def __init__(self, gpu: "Gpu", handle: int):
+        self.gpu = gpu
+        self._h = C.c_void_p(handle)
+        self.timing: Optional[FrameTiming] = None
+
+    def encode(self, name: str, buffers: Sequence[Buffer], params: Sequence[int],
+               threads: int, group_size: int, offsets: Optional[Sequence[int]] = None) -> None:
+        """DispatchEncoder::encode / encode_offsets (src/gpu.rs:120-141)."""
+        n = len(buffers)
+        bufs = (C.c_void_p * max(n, 1))(*[b.handle.value for b in buffers])
+        offs = None
+        if offsets is not None:
+            if len(offsets) != n:
+                raise QmrError(QMR_ERR_INVALID, f"{name}: offset count must match buffers")
+            offs = (C.c_size_t * max(n, 1))(*[int(o) for o in offsets])
+        _check(lib().qmr_encode(self._h, name.encode(), bufs, offs, n, _u32(params), len(params),
+                                threads, group_size))
+
+    def mark(self) -> int:
+        idx = C.c_int()
+        _check(lib().qmr_command_mark(self._h, C.byref(idx)))
+        return idx.value
+
+    def finish(self) -> FrameTiming:
+        t = _Timing()
+        _check(lib().qmr_command_finish(self._h, C.byref(t)))
+        self.timing = FrameTiming(t.cpu_encode_seconds, t.cpu_commit_seconds, t.gpu_seconds,
+                                  t.completion_wait_seconds)
+        return self.timing
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        v = C.c_double()
+        _check(lib().qmr_command_elapsed(self._h, a, b, C.byref(v)))
+        return v.value
+
+    def release(self) -> None:
+        if self._h:
+            lib().qmr_command_release(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        if _alive:
+            try:
+                self.release()
+            except Exception:
+                pass
+
+
+class Gpu:
+    """Gpu::new_with_variant (src/gpu.rs:305-437) on a HIP device."""
+
+    def __init__(self, variant: str = "aligned", reference: bool = False,
+                 metadata: str = "f32", block_matmul: Optional[str] = None,
+                 block_delta: Optional[str] = None, ordinal: int = 0):
+        opts = _Options(_s(variant), _s(metadata), _s(block_matmul), _s(block_delta),
+                        int(reference))
+        h = C.c_void_p()
+        _check(lib().qmr_device_open(ordinal, C.byref(opts), C.byref(h)))
+        self._h = h
+
+    # -- properties
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def name(self) -> str:
+        return lib().qmr_device_name(self._h).decode()
+
+    def kernel_mode(self) -> str:
+        return lib().qmr_kernel_mode(self._h).decode()
+
+    def metadata_mode(self) -> str:
+        return lib().qmr_metadata_mode(self._h).decode()
+
+    def block_kernel_mode(self) -> tuple[str, bool]:
+        m, d = C.c_int(), C.c_int()
+        lib().qmr_block_kernel_mode(self._h, C.byref(m), C.byref(d))
+        return BLOCK_MODE_NAMES[m.value], bool(d.value)
+
+    def set_block_kernel_mode(self, matmul: str, batched_delta: bool = True) -> None:
+        _check(lib().qmr_set_block_kernel_mode(self._h, BLOCK_MODES[matmul], int(batched_delta)))
+
+    def set_gemv_plan(self, rr: int = 0, ks: int = 0) -> None:
+        _check(lib().qmr_set_gemv_plan(self._h, rr, ks))
+
+    def gemv_plan(self, rows: int, cols: int, bits: int, batch: int) -> tuple[int, int]:
+        rr, ks = C.c_int(), C.c_int()
+        _check(lib().qmr_gemv_plan(self._h, rows, cols, bits, batch, C.byref(rr), C.byref(ks)))
+        return rr.value, ks.value
+
+    def last_kernel(self) -> str:
+        return lib().qmr_last_kernel(self._h).decode()
+
+    def max_lds(self) -> int:
+        return int(lib().qmr_device_max_lds(self._h))
+
+    def compact_metadata(self, bits: int, group: int, scales: np.ndarray, biases: np.ndarray):
+        s = np.ascontiguousarray(scales, dtype=np.float32)
+        b = np.ascontiguousarray(biases, dtype=np.float32)
+        so = np.empty(s.size, np.uint16)
+        bo = np.empty(b.size, np.uint16)
+        ok = lib().qmr_compact_metadata(self._h, bits, group, s.ctypes.data, b.ctypes.data,
+                                        s.size, so.ctypes.data, bo.ctypes.data)
+        return (so, bo) if ok else None
+
+    # -- buffers (src/gpu.rs:540-589)
+    def alloc(self, nbytes: int) -> Buffer:
+        h = C.c_void_p()
+        _check(lib().qmr_buffer_alloc(self._h, nbytes, C.byref(h)))
+        return Buffer(h.value)
+
+    def alloc_f32(self, n: int) -> Buffer:
+        return self.alloc(4 * n)
+
+    def upload_bytes(self, data) -> Buffer:
+        arr = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray))
+                                   else data)
+        h = C.c_void_p()
+        _check(lib().qmr_buffer_upload(self._h, arr.ctypes.data if arr.nbytes else None,
+                                       arr.nbytes, C.byref(h)))
+        return Buffer(h.value)
+
+    def upload_f32(self, values) -> Buffer:
+        return self.upload_bytes(np.ascontiguousarray(values, dtype=np.float32))
+
+    def read_f32(self, buf: Buffer, n: int, offset: int = 0) -> np.ndarray:
+        return buf.read(np.float32, n, offset)
+
+    # -- commands (src/gpu.rs:590-876)
+    def begin(self) -> Command:
+        h = C.c_void_p()
+        _check(lib().qmr_command_begin(self._h, C.byref(h)))
+        return Command(self, h.value)
+
+    def dispatch(self, name: str, buffers: Sequence[Buffer], params: Sequence[int],
+                 offsets: Optional[Sequence[int]] = None, group_size: int = 128) -> FrameTiming:
+        """One dispatch in its own command, with the layout's thread count."""
+        _, threads = dispatch_layout(name, params)
+        cmd = self.begin()
+        try:
+            cmd.encode(name, buffers, params, threads, group_size, offsets)
+            return cmd.finish()
+        finally:
+            cmd.release()
+
+    def close(self) -> None:
+        if self._h:
+            lib().qmr_device_close(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        if _alive:
+            try:
+                self.close()
+            except Exception:
+                pass

@@ -1,0 +1,92 @@
+"""BASELINE configurations at full size on the GPU against the FP64 oracle,
+with the BASELINE gate (rel-L2 <= 1e-5, max-abs <= 1e-4*max|y|), and bit-exact
+dequantisation of sampled rows:
+  1: Q4/g64 BF16 17408x5120 and 5120x17408, B=1
+  2: the same matrices, B=3 (MTP verification block)
+  3: Q8/g64 5120x5120 with F16 and with FP32 metadata; Q4/g64 BF16 head
+     151936x5120 at B=1 and B=3 (rows sampled for the oracle)
+  4: wide block 17408x5120 x 128 RHS (rows sampled for the oracle)
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import qmr.synth as synth
+from helpers import assert_gate, run_affine
+
+pytestmark = pytest.mark.gpu
+SEED = synth.DEFAULT_SEED
+THREADS = min(16, os.cpu_count() or 1)
+NAME = {"bf16": "_bf16", "f16": "_f16meta", "f32": ""}
+
+
+def rows_subset(m: synth.PackedMatrix, rows):
+    per_w = m.cols * m.bits // 32
+    per_m = m.cols // m.group
+    rows = np.asarray(rows)
+    w = m.w.reshape(m.rows, per_w)[rows].ravel()
+    s = m.s.reshape(m.rows, per_m)[rows].ravel()
+    b = m.b.reshape(m.rows, per_m)[rows].ravel()
+    return w, s, b
+
+
+def check(gpu, m, batch, sample_rows=None, name=None):
+    x = synth.activations(m.cols, batch, SEED, tag=f"cfg{m.rows}x{m.cols}")
+    name = name or (("matvec_affine" if batch == 1 else "matmul_affine") + NAME[m.meta])
+    got = run_affine(gpu, name, m.w, m.s, m.b, x, m.rows, m.cols, m.bits, m.group, batch)
+    if sample_rows is None:
+        want = oracle.matmul_f64(m.w, m.s, m.b, m.meta, x, m.rows, m.cols, m.bits, m.group, batch,
+                                 THREADS)
+        assert_gate(got, want, f"{synth.describe(m, batch)}")
+    else:
+        w, s, b = rows_subset(m, sample_rows)
+        want = oracle.matmul_f64(w, s, b, m.meta, x, len(sample_rows), m.cols, m.bits, m.group,
+                                 batch, THREADS)
+        got_s = np.concatenate([got[t * m.rows + np.asarray(sample_rows)] for t in range(batch)])
+        assert_gate(got_s, want, f"{synth.describe(m, batch)} sampled")
+    return got
+
+
+def check_dequant_rows(gpu, m, rows):
+    wb, sb, bb = (gpu.upload_bytes(a) for a in (m.w, m.s, m.b))
+    eb = gpu.alloc_f32(m.cols)
+    for r in rows:
+        gpu.dispatch("embed_affine" + NAME[m.meta], [wb, sb, bb, eb], [r, m.cols, m.bits, m.group])
+        got = gpu.read_f32(eb, m.cols)
+        want = oracle.dequant_row(m.w, m.s, m.b, m.meta, r, m.cols, m.bits, m.group)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"row {r}"
+
+
+@pytest.mark.parametrize("shape", ["gate_up", "down"])
+def test_config1_and_2_mlp_shapes(gpu, shape):
+    rows, cols = synth.MLP_SHAPES[shape]
+    m = synth.q4_bf16_matrix(rows, cols, SEED, tag=shape)
+    check(gpu, m, 1)
+    check(gpu, m, 3)
+    check_dequant_rows(gpu, m, [0, 1, rows // 2, rows - 1])
+
+
+def test_config3_q8_f16_and_f32_metadata(gpu):
+    m = synth.q8_f16_matrix(*synth.Q8_SHAPE, SEED)
+    check(gpu, m, 1)
+    check(gpu, synth.to_f32_metadata(m), 1)
+    check(gpu, m, 3)
+    check_dequant_rows(gpu, m, [0, 4095, 5119])
+
+
+def test_config3_vocabulary_head(gpu):
+    rows, cols = synth.HEAD_SHAPE
+    m = synth.q4_bf16_matrix(rows, cols, SEED, tag="head")
+    sample = sorted(set(list(range(0, rows, 97)) + [rows - 1]))
+    check(gpu, m, 1, sample)
+    check(gpu, m, 3, sample)
+    check_dequant_rows(gpu, m, [0, rows - 1])
+
+
+def test_config4_wide_block(gpu):
+    rows, cols = synth.MLP_SHAPES["gate_up"]
+    m = synth.q4_bf16_matrix(rows, cols, SEED, tag="gate_up")
+    sample = sorted(set(list(range(0, rows, 271)) + [rows - 1]))
+    check(gpu, m, 128, sample, name="matmul_affine_wide_bf16")

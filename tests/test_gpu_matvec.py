@@ -1,0 +1,167 @@
+"""GEMV parity on the GPU through the C ABI against the FP64 oracle.
+
+Restates the reference's GPU tests of its matvec pipelines:
+  src/gpu.rs:1637-1732            known answers (Q4 nibbles, Q8, dense, embeddings)
+  tests/quantized.rs:7-85         Q4/Q8 x groups x column/row tails x modes
+  tests/bf16_metadata.rs:7-99     the same grid with BF16 metadata + embeddings
+and adds the F16-metadata names, every compiled tiling of the GEMV kernel,
+and BASELINE config 0 against its committed golden vector.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+import qmr
+import qmr.synth as synth
+from helpers import (assert_close_ref, assert_gate, reference_metadata, reference_x, rotl,
+                     run_affine, to_bf16_truncated, xorshift_words)
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def test_affine_q4_little_nibbles_and_bias(gpus):
+    # src/gpu.rs:1637-1657
+    for mode, gpu in gpus.items():
+        w = gpu.upload_bytes(np.array([0x76543210, 0xFEDCBA98], np.uint32))
+        s = gpu.upload_f32([2.0, 0.5])
+        b = gpu.upload_f32([-1.0, -4.0])
+        x = gpu.upload_f32(np.ones(8))
+        y = gpu.alloc_f32(2)
+        cmd = gpu.begin()
+        cmd.encode("matvec_affine", [w, s, b, x, y], [2, 8, 4, 8], 64, 128)
+        cmd.finish()
+        assert gpu.read_f32(y, 2).tolist() == [48.0, 14.0], mode
+
+
+def test_dense_and_q8_matvec_and_embedding(gpu):
+    # src/gpu.rs:1699-1732
+    dense = np.array([1, 2, 3, 4, -1, 0, 1, 2], np.float16).view(np.uint16)
+    w = gpu.upload_bytes(dense)
+    x = gpu.upload_f32([1, 2, 3, 4])
+    y = gpu.alloc_f32(2)
+    gpu.dispatch("matvec_f16", [w, x, y], [2, 4])
+    np.testing.assert_allclose(gpu.read_f32(y, 2), [30, 10], rtol=3e-5)
+    emb = gpu.alloc_f32(4)
+    gpu.dispatch("embed_f16", [w, emb], [1, 4])
+    assert gpu.read_f32(emb, 4).tolist() == [-1, 0, 1, 2]
+    q = gpu.upload_bytes(np.array([0xFF800100, 0x04030201], np.uint32))
+    s = gpu.upload_f32([0.5, 2.0])
+    b = gpu.upload_f32([-1.0, -3.0])
+    gpu.dispatch("matvec_affine", [q, s, b, x, y], [2, 4, 8, 4])
+    np.testing.assert_allclose(gpu.read_f32(y, 2), [693, 30], rtol=3e-5)
+    gpu.dispatch("embed_affine", [q, s, b, emb], [0, 4, 8, 4])
+    assert gpu.read_f32(emb, 4).tolist() == [-1.0, -0.5, 63.0, 126.5]
+
+
+def _quantized_case(bits, group, cols, rows):
+    pack = 32 // bits
+    seed = 0x84213957 ^ bits ^ rotl(group, 7) ^ rotl(cols, 13) ^ rotl(rows, 19)
+    w = xorshift_words(seed, rows * cols // pack)
+    s, b = reference_metadata(rows * cols // group)
+    return w, s, b, reference_x(cols)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_specialized_q4_q8_match_scalar_across_groups_and_row_tails(gpus, bits, group):
+    # tests/quantized.rs:7-85: every mode, tolerance 2e-4 + 2e-5*|want|.
+    for cols in (group, 3 * group, 5120):
+        for rows in (1, 3, 7, 19, 20):
+            w, s, b, x = _quantized_case(bits, group, cols, rows)
+            want = oracle.matmul_f64(w, s, b, "f32", x, rows, cols, bits, group)
+            for mode, gpu in gpus.items():
+                got = run_affine(gpu, "matvec_affine", w, s, b, x, rows, cols, bits, group)
+                assert_close_ref(got, want, 2e-4, 2e-5, f"{mode} Q{bits}/g{group} {rows}x{cols}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("meta", ["bf16", "f16"])
+def test_16bit_metadata_matches_scalar_for_groups_shapes_and_embeddings(gpus, bits, group, meta):
+    # tests/bf16_metadata.rs:7-99, plus the same grid with F16 metadata.
+    name = "matvec_affine_bf16" if meta == "bf16" else "matvec_affine_f16meta"
+    embed = "embed_affine_bf16" if meta == "bf16" else "embed_affine_f16meta"
+    for cols in (group, 3 * group, 5120):
+        for rows in (1, 3, 7, 19, 20):
+            pack = 32 // bits
+            w = xorshift_words(0x1478ABCF, rows * cols // pack)
+            s, b = reference_metadata(rows * cols // group)
+            if meta == "bf16":
+                s16, b16 = to_bf16_truncated(s), to_bf16_truncated(b)
+            else:
+                s16, b16 = s.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+            x = reference_x(cols)
+            want = oracle.matmul_f64(w, s16, b16, meta, x, rows, cols, bits, group)
+            for mode in ("aligned", "packed4", "stream"):
+                gpu = gpus[mode]
+                got = run_affine(gpu, name, w, s16, b16, x, rows, cols, bits, group)
+                assert_close_ref(got, want, 2e-4, 2e-5, f"{mode} {name} Q{bits}/g{group} {rows}x{cols}")
+            gpu = gpus["aligned"]
+            wb, sb, bb = (gpu.upload_bytes(a) for a in (w, s16, b16))
+            eb = gpu.alloc_f32(cols)
+            gpu.dispatch(embed, [wb, sb, bb, eb], [rows - 1, cols, bits, group])
+            got = gpu.read_f32(eb, cols)
+            exact = oracle.dequant_row(w, s16, b16, meta, rows - 1, cols, bits, group)
+            assert np.array_equal(got.view(np.uint32), exact.view(np.uint32)), "embedding bits"
+
+
+def test_bf16_dispatch_is_unavailable_in_reference_mode(gpus):
+    gpu = gpus["reference"]
+    w = gpu.upload_bytes(np.zeros(64, np.uint32))
+    m = gpu.upload_bytes(np.zeros(8, np.uint16))
+    x = gpu.upload_f32(np.zeros(512))
+    y = gpu.alloc_f32(1)
+    with pytest.raises(qmr.QmrError, match="reference mode"):
+        gpu.dispatch("matvec_affine_bf16", [w, m, m, x, y], [1, 512, 4, 64])
+    with pytest.raises(qmr.QmrError, match="reference mode"):
+        gpu.dispatch("matmul_affine", [w, m, m, x, y], [1, 512, 4, 64, 1])
+
+
+PLANS = [(1, 1), (2, 1), (4, 1), (5, 2), (2, 2)]
+
+
+@pytest.mark.parametrize("rr,ks", PLANS)
+def test_every_compiled_tiling_matches_oracle(gpu, rr, ks):
+    """Each (rows-per-slot, K-split) instance, with row tails (rows not a
+    multiple of the tile), column tails (a partial round of chunks), both
+    code widths, the three metadata types and batches 1..4."""
+    gpu.set_gemv_plan(rr, ks)
+    try:
+        rng = np.random.default_rng(rr * 10 + ks)
+        for bits, meta, rows, cols in [(4, "bf16", 37, 1536), (4, "f32", 41, 64 * 17),
+                                       (8, "f16", 23, 1024 + 256), (4, "f16", 3, 5120),
+                                       (8, "bf16", 45, 64 * 9)]:
+            group = 64
+            pack = 32 // bits
+            w = rng.integers(0, 2**32, rows * cols // pack, dtype=np.uint32)
+            sf = rng.uniform(0.002, 0.02, rows * cols // group).astype(np.float32)
+            bf = (-(2 ** (bits - 1)) * sf + rng.normal(0, 1e-3, sf.size)).astype(np.float32)
+            if meta == "bf16":
+                s, b = synth.f32_to_bf16_bits(sf), synth.f32_to_bf16_bits(bf)
+            elif meta == "f16":
+                s, b = sf.astype(np.float16).view(np.uint16), bf.astype(np.float16).view(np.uint16)
+            else:
+                s, b = sf, bf
+            suffix = {"bf16": "_bf16", "f16": "_f16meta", "f32": ""}[meta]
+            for batch in (1, 2, 3, 4):
+                x = rng.standard_normal((batch, cols)).astype(np.float32)
+                want = oracle.matmul_f64(w, s, b, meta, x, rows, cols, bits, group, batch)
+                got = run_affine(gpu, "matmul_affine" + suffix, w, s, b, x, rows, cols, bits,
+                                 group, batch)
+                assert_gate(got, want, f"plan {rr},{ks} Q{bits} {meta} {rows}x{cols} B{batch}")
+    finally:
+        gpu.set_gemv_plan(0, 0)
+
+
+def test_config0_golden_meets_gate(gpu):
+    z = np.load(GOLDEN / "config0.npz")
+    seed = int(z["seed"])
+    m = synth.q4_bf16_matrix(1024, 1024, seed, tag="config0")
+    x = synth.activations(1024, 1, seed, tag="config0")
+    assert np.array_equal(m.w[:16], z["w_head"])
+    got = run_affine(gpu, "matvec_affine_bf16", m.w, m.s, m.b, x, 1024, 1024, 4, 64)
+    assert gpu.last_kernel() == "matvec_q4_g64_aligned_bf16"
+    assert_gate(got, z["y64"], "config 0")
