@@ -10,11 +10,12 @@ A step is one launch of the metric kernel over one synthetic input batch
 timed region starts. Weights rotate over --copies distinct copies so that the
 50 MB matrix is not served from the 256 MB Infinity Cache.
 
-Timing: each launch is bracketed by two HIP events recorded on the library's
-stream; the per-launch duration is their difference, and `value` is the
-algorithmic bytes of one launch (codes + scales + biases + x + y) divided by
-the mean duration. The wall time of the whole timed region (synchronised on
-both sides) gives ms_per_step.
+Timing: K launches run back to back between two HIP events recorded on the
+library's stream; their difference over K is the mean launch duration, and
+`value` is the algorithmic bytes of one launch (codes + scales + biases + x +
+y) divided by it. The wall time of that timed region (synchronised on both
+sides) gives ms_per_step. A second pass brackets each launch with its own
+events to report the spread.
 
 The CPU baseline times the FP64 oracle (the reference's per-weight
 dequantise-then-accumulate closure, restated in C) on this host.
@@ -46,35 +47,39 @@ def log(msg: str) -> None:
 
 
 def time_kernel(gpu: qmr.Gpu, name: str, bufsets, params, steps: int, warmup: int):
-    """Per-launch event durations (ms) and the wall time of the timed region."""
+    """Back-to-back launch timing (events at both ends of the timed region),
+    plus per-launch event brackets for the spread. Returns
+    (mean ms per launch back-to-back, wall seconds of that region,
+     per-launch bracketed durations in ms)."""
     _, threads = qmr.dispatch_layout(name, params)
     cmd = gpu.begin()
     for k in range(warmup):
         cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
     cmd.finish()
     cmd.release()
+    # Timed region: synchronised on both sides, K launches back to back.
     cmd = gpu.begin()
-    marks = []
     t0 = time.perf_counter()
-    for k in range(steps):
-        a = cmd.mark()
-        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
-        b = cmd.mark()
-        marks.append((a, b))
-    cmd.finish()
-    wall = time.perf_counter() - t0
-    durs = [cmd.elapsed_ms(a, b) for a, b in marks]
-    cmd.release()
-    # Back-to-back launches without inner events: stream throughput.
-    cmd = gpu.begin()
     a = cmd.mark()
     for k in range(steps):
         cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
     b = cmd.mark()
     cmd.finish()
-    stream_ms = cmd.elapsed_ms(a, b) / steps
+    wall = time.perf_counter() - t0
+    mean_ms = cmd.elapsed_ms(a, b) / steps
     cmd.release()
-    return durs, wall, stream_ms
+    # Spread: each launch bracketed by its own pair of events (adds the
+    # event overhead to every sample, so these read a little high).
+    cmd = gpu.begin()
+    marks = []
+    for k in range(min(steps, 100)):
+        a = cmd.mark()
+        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+        marks.append((a, cmd.mark()))
+    cmd.finish()
+    durs = [cmd.elapsed_ms(a, b) for a, b in marks]
+    cmd.release()
+    return mean_ms, wall, durs
 
 
 def cpu_baseline(m: synth.PackedMatrix, budget_s: float) -> dict:
@@ -176,24 +181,22 @@ def main() -> int:
             name = "matvec_affine_bf16" if batch == 1 else "matmul_affine_bf16"
             params = [rows, cols, 4, 64] + ([batch] if batch > 1 else [])
             log(f"bench: {tag} {rows}x{cols} B={batch} ({name})")
-            durs, wall, stream_ms = time_kernel(gpu, name, bufsets, params, args.steps, args.warmup)
+            mean_ms, wall, durs = time_kernel(gpu, name, bufsets, params, args.steps, args.warmup)
             nbytes = synth.algorithmic_bytes(m, batch)
-            mean_ms = statistics.fmean(durs)
-            med_ms = statistics.median(durs)
-            q = np.quantile(durs, [0.1, 0.9])
+            q = np.quantile(durs, [0.1, 0.5, 0.9])
             r = {
                 "shape": f"{rows}x{cols}", "tag": tag, "batch": batch, "kernel": gpu.last_kernel(),
                 "plan": list(gpu.gemv_plan(rows, cols, 4, batch)),
-                "us_mean": round(mean_ms * 1e3, 3), "us_median": round(med_ms * 1e3, 3),
-                "us_p10": round(q[0] * 1e3, 3), "us_p90": round(q[1] * 1e3, 3),
-                "us_stream": round(stream_ms * 1e3, 3),
+                "us_mean": round(mean_ms * 1e3, 3),
+                "us_bracketed_p10_p50_p90": [round(v * 1e3, 3) for v in q],
                 "algorithmic_bytes": nbytes,
                 "gbps": round(nbytes / (mean_ms * 1e-3) / 1e9, 1),
                 "frac_peak": round(nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
             }
-            log(f"bench:   {r['us_mean']} us mean ({r['us_median']} median, {r['us_stream']} "
-                f"back-to-back), {r['gbps']} GB/s = {100 * r['frac_peak']:.1f}% of peak")
+            log(f"bench:   {r['us_mean']} us per launch back-to-back (bracketed p50 "
+                f"{r['us_bracketed_p10_p50_p90'][1]}), {r['gbps']} GB/s = "
+                f"{100 * r['frac_peak']:.1f}% of peak")
             results.append(r)
             del bufsets, ys, xb
         del mats

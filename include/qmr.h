@@ -173,8 +173,10 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  */
 
 /* ---- Testing and tuning hooks (no counterpart in the reference). ---- */
-/* Force the GEMV tiling (rows per slot `rr`, K-split `ks`; 0,0 = planner).
- * Only compiled pairs are accepted; others fall back to the planner. */
+/* Force the GEMV tiling: rr = -1 selects the streaming single-RHS kernel
+ * (blocks then use the planner's row-slot tiling); rr > 0 with ks > 0
+ * selects the row-slot kernel with `rr` rows per slot and a K-split of
+ * `ks`; 0,0 = planner. Pairs that are not compiled fall back to the planner. */
 int qmr_set_gemv_plan(qmr_device *device, int rr, int ks);
 /* The plan the GEMV launcher uses for a shape (honours a forced plan). */
 int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32_t bits,

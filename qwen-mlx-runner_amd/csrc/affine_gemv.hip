@@ -64,7 +64,6 @@ __device__ __forceinline__ float load_meta(const void *p, size_t i) {
 
 // DPP / swizzle butterfly over each 32-lane half of the wave. Every lane ends
 // with its half-wave's total; the order of additions is fixed.
-__device__ __forceinline__ float dpp_f(float v, int ctrl);
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
@@ -314,6 +313,204 @@ __global__ __launch_bounds__(kThreads) void affine_gemv_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming variant: one 16-wave workgroup per CU (32 half-wave slots).
+//
+// A workgroup owns R consecutive rows and all T rounds of them. Its T*R
+// (round, row) units are numbered round-major and dealt to the 32 slots in
+// contiguous, equal runs (R*T/32 units each, +-1), so every slot streams the
+// same number of bytes and mostly walks down rows at one fixed round: the x
+// chunk it reads from LDS is reused across its whole run. Each slot keeps P
+// units of loads in flight in a register ring (weights, scale, bias), issued
+// before x is staged, so the workgroup's first HBM requests leave at once
+// and the ring then refills one unit behind each unit consumed. A unit's
+// lane partials are reduced across the slot (DPP + swizzle) and parked in
+// LDS at [round][row]; after a barrier every row is summed over its rounds in
+// round order, so the result is deterministic.
+// ---------------------------------------------------------------------------
+constexpr int kUThreads = 1024;
+constexpr int kUSlots = kUThreads / 32;
+
+template <int B>
+struct Ring {
+    uint32_t w[4];
+    float s, b;
+};
+
+template <int BITS, int META, int B, int P, bool XLDS>
+__global__ __launch_bounds__(kUThreads) void affine_gemv_units_kernel(
+    const uint32_t *__restrict__ w, const void *__restrict__ sp, const void *__restrict__ bp,
+    const float *__restrict__ x, float *__restrict__ y, uint32_t rows, uint32_t cols,
+    uint32_t group_shift, uint32_t vec16, uint32_t rows_per_wg) {
+    using G = Geo<BITS>;
+    constexpr int kUnits = G::kUnits;
+    extern __shared__ float4 lds4[];
+    const uint32_t C = cols / G::kChunkCols;
+    const uint32_t T = (C + 31) / 32;
+    const uint32_t units4 = cols / 4;
+    const uint32_t r0 = blockIdx.x * rows_per_wg;
+    const uint32_t R = rows - r0 < rows_per_wg ? rows - r0 : rows_per_wg;
+    float4 *xs = lds4;
+    float *xsum = reinterpret_cast<float *>(lds4 + (XLDS ? B * units4 : 0));  // [B][C]
+    float *part = xsum + B * C;                                                // [B][T][rows_per_wg]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 31;
+    const int slot = tid >> 5;
+    const uint32_t n_units = T * R;
+    const uint32_t u_begin = uint32_t(uint64_t(n_units) * slot / kUSlots);
+    const uint32_t u_end = uint32_t(uint64_t(n_units) * (slot + 1) / kUSlots);
+    const uint32_t groups = cols >> group_shift;
+
+    // Issue cursor (it, ir) and compute cursor (ct, cr) over round-major units.
+    uint32_t it = u_begin / R, ir = u_begin % R;
+    uint32_t ct = it, cr = ir;
+
+    Ring<B> ring[P];
+    auto issue = [&](Ring<B> &sl, bool active) {
+        const uint32_t chunk = it * 32 + lane;
+        const uint32_t row = r0 + ir;
+        if (active && chunk < C) {
+            const uint32_t *src = w + (size_t(row) * C + chunk) * 4;
+            if (vec16) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(src);
+                sl.w[0] = v.x;
+                sl.w[1] = v.y;
+                sl.w[2] = v.z;
+                sl.w[3] = v.w;
+            } else {
+                sl.w[0] = src[0];
+                sl.w[1] = src[1];
+                sl.w[2] = src[2];
+                sl.w[3] = src[3];
+            }
+            const size_t gi = size_t(row) * groups + ((chunk * G::kChunkCols) >> group_shift);
+            sl.s = load_meta<META>(sp, gi);
+            sl.b = load_meta<META>(bp, gi);
+        } else {
+            sl.w[0] = sl.w[1] = sl.w[2] = sl.w[3] = 0u;
+            sl.s = 0.f;
+            sl.b = 0.f;
+        }
+        if (++ir == R) {
+            ir = 0;
+            ++it;
+        }
+    };
+
+#pragma unroll
+    for (int j = 0; j < P; ++j) issue(ring[j], u_begin + j < u_end);
+
+    // Stage x and per-chunk sums while the first weight loads are in flight.
+    for (uint32_t ck = tid; ck < B * C; ck += kUThreads) {
+        const uint32_t t = ck / C, chunk = ck % C;
+        const float *src = x + size_t(t) * cols + size_t(chunk) * G::kChunkCols;
+        float sum = 0.f;
+#pragma unroll
+        for (int u = 0; u < kUnits; ++u) {
+            const float4 v = make_float4(src[4 * u], src[4 * u + 1], src[4 * u + 2], src[4 * u + 3]);
+            sum += v.x;
+            sum += v.y;
+            sum += v.z;
+            sum += v.w;
+            if constexpr (XLDS) xs[t * units4 + swz<BITS>(chunk * kUnits + u)] = v;
+        }
+        xsum[ck] = sum;
+    }
+    __syncthreads();
+
+    float4 xv[B][kUnits];
+    float xsv[B];
+    uint32_t cur_t = 0xFFFFFFFFu;
+    for (uint32_t base = u_begin; base < u_end; base += P) {
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            const uint32_t u = base + j;
+            if (u < u_end) {
+                const uint32_t chunk = ct * 32 + lane;
+                const bool cv = chunk < C;
+                if (ct != cur_t) {
+                    cur_t = ct;
+#pragma unroll
+                    for (int t = 0; t < B; ++t) {
+                        if (cv) {
+                            if constexpr (XLDS) {
+#pragma unroll
+                                for (int k = 0; k < kUnits; ++k)
+                                    xv[t][k] = xs[t * units4 + swz<BITS>(chunk * kUnits + k)];
+                            } else {
+                                const float *src = x + size_t(t) * cols + size_t(chunk) * G::kChunkCols;
+#pragma unroll
+                                for (int k = 0; k < kUnits; ++k)
+                                    xv[t][k] = make_float4(src[4 * k], src[4 * k + 1], src[4 * k + 2],
+                                                           src[4 * k + 3]);
+                            }
+                            xsv[t] = xsum[t * C + chunk];
+                        } else {
+#pragma unroll
+                            for (int k = 0; k < kUnits; ++k) xv[t][k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                            xsv[t] = 0.f;
+                        }
+                    }
+                }
+                const Ring<B> &sl = ring[j];
+                const float s24 = sl.s * 16777216.0f;  // 2^24, exact
+#pragma unroll
+                for (int t = 0; t < B; ++t) {
+                    float ae = 0.f, ao = 0.f, q;
+                    if constexpr (BITS == 4) {
+                        q4_chunk(sl.w, xv[t], ae, ao);
+                        q = __builtin_fmaf(ao, 0.0625f, ae);
+                    } else {
+                        q8_chunk(sl.w, xv[t], ae, ao);
+                        q = ae + ao;
+                    }
+                    float p = __builtin_fmaf(sl.b, xsv[t], s24 * q);
+                    p = half_wave_sum(p);
+                    if (lane == 0) part[(t * T + ct) * rows_per_wg + cr] = p;
+                }
+                if (++cr == R) {
+                    cr = 0;
+                    ++ct;
+                }
+            }
+            if (u + P < u_end) issue(ring[j], true);
+        }
+    }
+    __syncthreads();
+    for (uint32_t idx = tid; idx < R * B; idx += kUThreads) {
+        const uint32_t t = idx / R, r = idx % R;
+        const float *pp = part + size_t(t) * T * rows_per_wg + r;
+        float v = pp[0];
+        for (uint32_t k = 1; k < T; ++k) v += pp[size_t(k) * rows_per_wg];
+        y[size_t(t) * rows + r0 + r] = v;
+    }
+}
+
+template <int BITS, int META, int B, int P, bool XLDS>
+hipError_t launch_units(const AffineArgs &a, hipStream_t stream, size_t lds_bytes, uint32_t group_shift,
+                        uint32_t vec16, uint32_t rows_per_wg) {
+    auto kernel = affine_gemv_units_kernel<BITS, META, B, P, XLDS>;
+    static size_t configured = 0;
+    if (lds_bytes > 65536 && lds_bytes > configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           int(lds_bytes));
+        if (e != hipSuccess) return e;
+        configured = lds_bytes;
+    }
+    const uint32_t blocks = (a.rows + rows_per_wg - 1) / rows_per_wg;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kUThreads), lds_bytes, stream, a.w, a.s, a.b, a.x,
+                       a.y, a.rows, a.cols, group_shift, vec16, rows_per_wg);
+    return hipGetLastError();
+}
+
+template <int BITS, int META, int B, bool XLDS>
+hipError_t units_meta(const AffineArgs &a, hipStream_t stream, size_t lds, uint32_t gs,
+                      uint32_t vec16, uint32_t rpw) {
+    return launch_units<BITS, META, B, 8, XLDS>(a, stream, lds, gs, vec16, rpw);
+}
+
 template <int BITS, int META, int B, int RR, int KS, bool XLDS>
 hipError_t launch_instance(const AffineArgs &a, hipStream_t stream, size_t lds_bytes,
                            uint32_t group_shift, uint32_t vec16) {
@@ -379,14 +576,16 @@ size_t lds_bytes_for(const AffineArgs &a, GemvPlan p, bool xlds) {
 }  // namespace
 
 GemvPlan plan_affine_gemv(const AffineArgs &a, GemvPlan forced, const DeviceLimits &lim) {
+    if (forced.rr == -1) return {-1, 0};
     if (forced.rr > 0 && forced.ks > 0) {
         for (auto &pp : kPlans)
             if (pp[0] == forced.rr && pp[1] == forced.ks) return forced;
     }
-    // Rounds of 32 chunks per row and rows per CU decide the tiling: long
-    // rows with few of them per CU (down-projection shapes) split K across
-    // two slots so that a workgroup of 20 rows covers one CU; tall matrices
-    // keep whole rows per slot.
+    // Single-RHS products stream through CU-sized workgroups (rr = -1).
+    if (a.batch == 1) return {-1, 0};
+    // Blocks keep the row-slot kernel: long rows with few of them per CU
+    // split K across two slots so that a workgroup of 20 rows covers one CU;
+    // tall matrices keep whole rows per slot.
     const uint32_t chunk_cols = 128 / a.bits;
     const uint32_t rounds = (a.cols / chunk_cols + 31) / 32;
     const double rows_per_cu = double(a.rows) / double(lim.num_cus > 0 ? lim.num_cus : 256);
@@ -405,13 +604,56 @@ GemvPlan plan_affine_gemv(const AffineArgs &a, GemvPlan forced, const DeviceLimi
     return p;
 }
 
+namespace {
+
+template <int BITS, int META>
+hipError_t units_b(const AffineArgs &a, hipStream_t stream, bool xlds, size_t lds, uint32_t gs,
+                   uint32_t vec16, uint32_t rpw) {
+    if (a.batch != 1) return hipErrorInvalidValue;
+    return xlds ? units_meta<BITS, META, 1, true>(a, stream, lds, gs, vec16, rpw)
+                : units_meta<BITS, META, 1, false>(a, stream, lds, gs, vec16, rpw);
+}
+
+hipError_t launch_units_kernel(const AffineArgs &a, const DeviceLimits &lim, hipStream_t stream,
+                               uint32_t gs, uint32_t vec16) {
+    const uint32_t cus = lim.num_cus > 0 ? uint32_t(lim.num_cus) : 256u;
+    const uint32_t grid = a.rows < cus ? a.rows : cus;
+    const uint32_t rpw = (a.rows + grid - 1) / grid;
+    const size_t C = a.cols / (128 / a.bits);
+    const size_t T = (C + 31) / 32;
+    size_t lds = size_t(a.batch) * (C + T * rpw) * 4;
+    bool xlds = true;
+    if (lds + size_t(a.batch) * a.cols * 4 <= lim.max_lds_per_block) {
+        lds += size_t(a.batch) * a.cols * 4;
+    } else {
+        xlds = false;
+        if (lds > lim.max_lds_per_block) return hipErrorInvalidValue;
+    }
+    const int meta = static_cast<int>(a.meta);
+    if (a.bits == 4) {
+        if (meta == 0) return units_b<4, 0>(a, stream, xlds, lds, gs, vec16, rpw);
+        if (meta == 1) return units_b<4, 1>(a, stream, xlds, lds, gs, vec16, rpw);
+        return units_b<4, 2>(a, stream, xlds, lds, gs, vec16, rpw);
+    }
+    if (meta == 0) return units_b<8, 0>(a, stream, xlds, lds, gs, vec16, rpw);
+    if (meta == 1) return units_b<8, 1>(a, stream, xlds, lds, gs, vec16, rpw);
+    return units_b<8, 2>(a, stream, xlds, lds, gs, vec16, rpw);
+}
+
+}  // namespace
+
 hipError_t launch_affine_gemv(const AffineArgs &a, GemvPlan forced, const DeviceLimits &lim,
                               hipStream_t stream) {
-    const GemvPlan p = plan_affine_gemv(a, forced, lim);
+    GemvPlan p = plan_affine_gemv(a, forced, lim);
     uint32_t gs = 0;
     while ((1u << gs) < a.group) ++gs;
     if ((1u << gs) != a.group) return hipErrorInvalidValue;
     const uint32_t vec16 = (reinterpret_cast<uintptr_t>(a.w) & 15) == 0 ? 1u : 0u;
+    if (p.rr == -1) {
+        if (a.batch == 1) return launch_units_kernel(a, lim, stream, gs, vec16);
+        p = plan_affine_gemv(a, GemvPlan{}, lim);  // blocks use the row-slot kernel
+        if (p.rr == -1) p = {1, 1};
+    }
     bool xlds = true;
     size_t lds = lds_bytes_for(a, p, true);
     if (lds > lim.max_lds_per_block) {

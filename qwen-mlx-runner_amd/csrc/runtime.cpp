@@ -127,7 +127,8 @@ int qmr_device_open(int ordinal, const qmr_device_options *options, qmr_device *
                "Kernels are built for gfx950 (MI355X); device reports " + arch, QMR_ERR_DEVICE);
         auto *dev = new qmr_device();
         dev->ordinal = ordinal;
-        dev->name = prop.name;
+        dev->name = prop.name[0] ? std::string(prop.name)
+                                  : "AMD Instinct " + arch.substr(0, arch.find(':'));
         dev->gemv_variant = variant;
         dev->reference = opt.reference != 0;
         dev->bf16_metadata = metadata == "bf16" && !dev->reference;

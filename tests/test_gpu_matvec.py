@@ -120,7 +120,7 @@ def test_bf16_dispatch_is_unavailable_in_reference_mode(gpus):
         gpu.dispatch("matmul_affine", [w, m, m, x, y], [1, 512, 4, 64, 1])
 
 
-PLANS = [(1, 1), (2, 1), (4, 1), (5, 2), (2, 2)]
+PLANS = [(-1, 0), (1, 1), (2, 1), (4, 1), (5, 2), (2, 2)]
 
 
 @pytest.mark.parametrize("rr,ks", PLANS)
@@ -130,7 +130,7 @@ def test_every_compiled_tiling_matches_oracle(gpu, rr, ks):
     code widths, the three metadata types and batches 1..4."""
     gpu.set_gemv_plan(rr, ks)
     try:
-        rng = np.random.default_rng(rr * 10 + ks)
+        rng = np.random.default_rng(abs(rr) * 10 + ks + (rr < 0))
         for bits, meta, rows, cols in [(4, "bf16", 37, 1536), (4, "f32", 41, 64 * 17),
                                        (8, "f16", 23, 1024 + 256), (4, "f16", 3, 5120),
                                        (8, "bf16", 45, 64 * 9)]:
