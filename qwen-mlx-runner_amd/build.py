@@ -28,6 +28,7 @@ SOURCES = [
     ("contract.cpp", ["-x", "c++"]),
     ("runtime.cpp", ["-x", "hip"]),
     ("affine_gemv.hip", ["-x", "hip"]),
+    ("affine_mfma.hip", ["-x", "hip"]),
     ("misc_kernels.hip", ["-x", "hip"]),
     ("wide_mfma.hip", ["-x", "hip"]),
 ]

@@ -1,0 +1,674 @@
+// Streaming dequantise + GEMV / small block (batch 1..4) over MLX affine
+// packed weights on the gfx950 matrix cores.
+//
+// Computes, for every RHS t < B and output row r,
+//     y[t*rows + r] = sum_g ( s[r,g] * sum_{c in g} q[r,c] * x[t,c]
+//                           + b[r,g] * sum_{c in g} x[t,c] )
+// which is the reference's per-weight affine dot (kernels/qwen.metal:40-68,
+// kernels/matmul_block.metal:20-79) in the factored form of
+// kernels/matvec_fast.metal:11-15.
+//
+// Why MFMA for a memory-bound product. Dequantising on the vector ALU costs
+// one FMA per weight per RHS plus the unpack (about 1.6 lane-ops per weight
+// at B=1 and 4.6 at B=3), while HBM delivers Q4/g64 at about 1.4e13 weights/s
+// against 3.9e13 VALU lane-ops/s: B=3 would be ALU-bound. Here the unpack is
+// the only per-weight ALU work (7 ops per 8 codes, for any B up to 4); the
+// products run on v_mfma_f32_16x16x32_f16, which has more than 10x headroom.
+//
+// Exactness. A Q4 code shifted into bits 4-7 of a 16-bit half is an IEEE
+// half subnormal of value q*2^-20, a Q8 byte in bits 2-9 is q*2^-22: exact
+// f16 operands (see the note at unpack() on why not bits 0-3). Activations
+// are split x*2^-e = hi + lo into two f16 values (about 22 significant bits
+// together, with a power-of-two scale 2^-e per RHS chosen from the block's
+// max |x| so that neither part overflows or loses range); the matrix core multiplies
+// exactly and accumulates in FP32. The scale factors 2^20 or 2^22 (code
+// encoding) and 2^e (activation scale) are restored exactly in the FP32
+// epilogue.
+//
+// Operand placement (16x16x32 f16: A row i = lane%16, B column j = lane%16,
+// both taking K chunk lane/16; D[i][j] lives in lane j + 16*(i/4), element
+// i%4):
+//   B operand = codes: lane (r, g) holds 8 codes of weight row r (one u32
+//     word for Q4, two for Q8) from K chunk g.
+//   A operand = activations: row i is a "slot" (group gamma, RHS t, part
+//     hi/lo); it is non-zero only on the K chunks that belong to quant group
+//     gamma, so one MFMA keeps the partial dots of different quant groups in
+//     different D rows and the per-group scale can be applied afterwards.
+// A tile is 16 rows x 128 K: each lane loads 16 B (Q4) or 32 B (Q8) of codes
+// with one or two 128-bit buffer loads, plus its group's scale and bias; four
+// MFMAs consume the tile. Lane (r, g) of D holds the four slots of one quant
+// group and row r, i.e. exactly the group whose scale/bias that lane loaded,
+// so the epilogue is four FMAs for the scales and two for the biases.
+//
+// Work decomposition. A wave owns one 16-row tile and a contiguous range of
+// K tiles; a workgroup holds RT waves (RT row tiles) over the same K range
+// and stages that range of x once in LDS, already split into hi/lo f16 in
+// MFMA operand order, with the per-group sums of x. A matrix is covered by
+// nbands x ns workgroups (row bands x K splits). With ns > 1 each workgroup
+// writes its partial sums to a workspace; the last workgroup of a band to
+// finish (an atomic counter) adds the ns partials in split order and writes
+// y, so results do not depend on timing. Each lane keeps P tiles of loads in
+// flight in a register ring; the first P tiles are requested before x is
+// staged.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "kernels.hpp"
+
+namespace qmr {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTileK = 128;             // K per tile
+constexpr uint32_t kOut = 0x80000000u;  // buffer offset past every range: loads return 0
+constexpr uint32_t kRsrcWord3 = 0x00020000u;
+constexpr int kAuxStream = 2;           // nt: streaming weights
+constexpr int kMaxRt = 8;
+constexpr int kItems = 2;       // staged x slices per thread: tps * B * 16 <= kItems * 64 * rt
+constexpr int kMetaUnits = 5;   // staged metadata loads per thread: ceil(tps*NGM/UE) <= 4 * kMetaUnits
+constexpr uint32_t kMaxSplits = 16;  // K splits across workgroups
+
+struct MfmaParams {
+    const uint32_t *w;
+    const void *s;
+    const void *b;
+    const float *x;
+    float *y;
+    float *partial;      // [ns][B][rows] when ns > 1
+    uint32_t *counters;  // [nbands] when ns > 1, zero between launches
+    uint32_t rows, cols;
+    uint32_t w_bytes, m_bytes;  // extents of the code and metadata views
+    uint32_t nbands, ns, tiles, tps;
+};
+
+template <int META>
+__device__ __forceinline__ float meta_f32(uint32_t v) {
+    if constexpr (META == 0) {
+        return __uint_as_float(v);
+    } else if constexpr (META == 1) {
+        return __uint_as_float(v << 16);
+    } else {
+        return float(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v)));
+    }
+}
+
+// Code encoding. A code is placed inside a 16-bit half so that the half is an
+// IEEE f16 subnormal of value q * 2^-CODE_EXP. The matrix core rounds
+// products of the smallest subnormals (codes in bits 0-3, q * 2^-24) with a
+// biased error near 2^-22 of the dot product, while codes at bits 4-7 (Q4,
+// q * 2^-20) or bits 2-9 (Q8, q * 2^-22) are as accurate as normal f16
+// operands (about 2^-27 relative to the sum of |products|, unbiased); bits
+// 10-14 are the exponent, so no higher placement is linear in q.
+//   Q4 word -> halves [q0, q4 | q1, q5 | q2, q6 | q3, q7] * 2^-20
+//   Q8 words w0,w1 -> [b0, b2 | b1, b3 | b4, b6 | b5, b7] * 2^-22
+// k_of(e) is the column (within the 8-column chunk) of half e.
+template <int BITS>
+constexpr int kCodeExp = BITS == 4 ? 20 : 22;
+
+template <int BITS>
+__device__ __forceinline__ int k_of(int e) {
+    if constexpr (BITS == 4) {
+        constexpr int k[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+        return k[e];
+    } else {
+        constexpr int k[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+        return k[e];
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ h8 unpack(const u4 (&c)[BITS / 4], int m) {
+    u4 v;
+    if constexpr (BITS == 4) {
+        const uint32_t wd = c[0][m];
+        v[0] = (wd << 4) & 0x00F000F0u;
+        v[1] = wd & 0x00F000F0u;
+        v[2] = (wd >> 4) & 0x00F000F0u;
+        v[3] = (wd >> 8) & 0x00F000F0u;
+    } else {
+        const uint32_t w0 = c[(2 * m) >> 2][(2 * m) & 3];
+        const uint32_t w1 = c[(2 * m + 1) >> 2][(2 * m + 1) & 3];
+        v[0] = (w0 << 2) & 0x03FC03FCu;
+        v[1] = (w0 >> 6) & 0x03FC03FCu;
+        v[2] = (w1 << 2) & 0x03FC03FCu;
+        v[3] = (w1 >> 6) & 0x03FC03FCu;
+    }
+    return __builtin_bit_cast(h8, v);
+}
+
+// Workgroup barrier ordering LDS only: outstanding global loads (the weight
+// ring) stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int META>
+__device__ __forceinline__ float meta_lo(uint32_t v) {  // entry packed as s | b << 16
+    if constexpr (META == 1) return __uint_as_float(v << 16);
+    return float(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v & 0xFFFFu)));
+}
+template <int META>
+__device__ __forceinline__ float meta_hi(uint32_t v) {
+    if constexpr (META == 1) return __uint_as_float(v & 0xFFFF0000u);
+    return float(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v >> 16)));
+}
+
+// Order this wave's earlier global writes before what follows, without the
+// device-scope fence (which writes back and invalidates the L2). Visibility
+// across XCDs comes from the agent-scope atomic stores and loads, which go
+// through the caches.
+__device__ __forceinline__ void vmem_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
+}
+
+template <int BITS, int META, int GROUP, int B, int P, bool PAIRS>
+__global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) {
+    constexpr int NGM = kTileK / GROUP;  // quant groups per tile
+    constexpr int SLOTS = 16 / NGM;      // A rows per quant group
+    constexpr int HALF = SLOTS / 2;      // RHS per quant group in D (>= B)
+    constexpr int NLD = BITS / 4;        // 128-bit code loads per lane per tile
+    constexpr int MB = META == 0 ? 4 : 2;
+    constexpr int MW = META == 0 ? 2 : 1;  // LDS words per metadata entry
+    constexpr int UE = PAIRS ? 2 : 1;      // entries per staged metadata load
+    constexpr int LANE_BYTES = BITS * 4;   // code bytes of one K chunk (32 codes)
+    constexpr int TPE = 8 / BITS;          // K tiles per 128-byte entry
+    static_assert(2 * B <= SLOTS, "batch does not fit the slot layout");
+    static_assert(!PAIRS || MB == 2, "paired metadata loads need 16-bit entries");
+
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int tid = threadIdx.x;
+    const int nthr = blockDim.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int r = lane & 15;
+    const int lg = lane >> 4;
+    const uint32_t RT = uint32_t(nthr) >> 6;
+    const uint32_t band = blockIdx.x % p.nbands;
+    const uint32_t split = blockIdx.x / p.nbands;
+    const uint32_t T0 = split * p.tps;
+    const uint32_t T1 = min(T0 + p.tps, p.tiles);
+    const uint32_t nT = T1 - T0;
+    const uint32_t G = nT * NGM;                    // metadata entries per row in this split
+    const uint32_t Gp = (p.tps * NGM + 1) | 1;      // their LDS pitch (odd: spreads banks)
+    const uint32_t band_row0 = band * RT * 16;
+
+    u4 *ldsA = reinterpret_cast<u4 *>(lds);  // [tps][4 m][4 g][2B] operand blocks
+    float4 *ldsSx = reinterpret_cast<float4 *>(lds + size_t(p.tps) * 4 * 4 * 2 * B * 16);
+    // ldsSx [tps][NGM][HALF/2]: (sum x_t, sum x_t+1, 2^(c+e_t), 2^(c+e_t+1)) per RHS pair
+    uint32_t *ldsM = reinterpret_cast<uint32_t *>(ldsSx + size_t(p.tps) * NGM * (HALF / 2));
+    // ldsM [RT*16 rows][Gp] entries: s | b << 16 (16-bit) or (s, b) as two words
+    int *ldsLast = reinterpret_cast<int *>(ldsM + size_t(RT) * 16 * Gp * MW);
+
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(p.w), 0, int(p.w_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.s), 0, int(p.m_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t br =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.b), 0, int(p.m_bytes), kRsrcWord3);
+
+    // ---- 1. Metadata of the band's rows over this K range (to LDS below). ----
+    // Rows past the matrix read zeros through the buffer range check.
+    const uint32_t m_pitch = p.cols / GROUP;
+    const uint32_t units_per_row = (G + UE - 1) / UE;
+    const uint32_t units = RT * 16 * units_per_row;
+    uint32_t mv_s[kMetaUnits], mv_b[kMetaUnits];
+#pragma unroll
+    for (int u = 0; u < kMetaUnits; ++u) {
+        const uint32_t f = tid + u * nthr;
+        const uint32_t rl = f / units_per_row;
+        const uint32_t gu = f - rl * units_per_row;
+        const uint32_t off = f < units ? ((band_row0 + rl) * m_pitch + T0 * NGM + gu * UE) * MB : kOut;
+        if constexpr (MB == 4 || PAIRS) {
+            mv_s[u] = __builtin_amdgcn_raw_buffer_load_b32(sr, int(off), 0, 0);
+            mv_b[u] = __builtin_amdgcn_raw_buffer_load_b32(br, int(off), 0, 0);
+        } else {
+            mv_s[u] = __builtin_amdgcn_raw_buffer_load_b16(sr, int(off), 0, 0);
+            mv_b[u] = __builtin_amdgcn_raw_buffer_load_b16(br, int(off), 0, 0);
+        }
+    }
+
+    // ---- 2. This thread's slices of x. Item = (tile Tl, RHS t, K chunk g,
+    // MFMA m): 8 consecutive columns; the GROUP/8 items of one quant group sit
+    // in consecutive lanes. ----
+    const uint32_t items = nT * B * 16;
+    float xv[kItems][8];
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const uint32_t it = tid + i * nthr;
+        const uint32_t tt = it >> 4;
+        const uint32_t k = (T0 + tt / B) * kTileK + 32u * ((it >> 2) & 3) + 8u * (it & 3);
+        const float *xs = p.x + size_t(tt % B) * p.cols;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[i][j] = (it < items && k + j < p.cols) ? xs[k + j] : 0.f;
+    }
+
+    // ---- 3. The first P entries of codes, requested in ring order. ----
+    // An entry is 128 contiguous bytes of each of the wave's 16 rows (TPE
+    // K tiles), read with two 128-bit loads per lane: the first covers rows
+    // 0-7 and the second rows 8-15, eight lanes per row. A lane (r, g) keeps
+    // the piece of its own row that the MFMA layout gives it (kp) and fetches
+    // for lane r^8 the piece that lane needs from the other half (sp); the
+    // two swap through DPP after the loads land.
+    const uint32_t row = band_row0 + wave * 16 + r;
+    const bool row_ok = row < p.rows;
+    const bool lo_half = r < 8;
+    const uint32_t kp = BITS == 4 ? uint32_t(lg) : 2u * lg;       // 16-byte piece kept
+    const uint32_t sp = BITS == 4 ? uint32_t(lg) + 4 : 2u * lg + 1;  // piece sent to lane r^8
+    const uint32_t piece1 = lo_half ? kp : sp;  // load 1 (rows 0-7)
+    const uint32_t piece2 = lo_half ? sp : kp;  // load 2 (rows 8-15)
+    const uint32_t row_bytes = p.cols / 32 * LANE_BYTES;
+    const uint32_t tile0 = band_row0 + wave * 16;
+    const uint32_t base1 = (tile0 + (r & 7)) * row_bytes + 16 * piece1;
+    const uint32_t base2 = (tile0 + 8 + (r & 7)) * row_bytes + 16 * piece2;
+    // Bytes of each row this split may read: min(row end, split end).
+    const uint32_t end_b = min(row_bytes, T1 * (4 * LANE_BYTES));
+    const uint32_t E0 = T0 / TPE;  // first entry (tps is a multiple of TPE)
+    auto issue = [&](u4 (&c)[2], uint32_t E) {
+        const uint32_t eb = E * 128;
+        const uint32_t o1 = eb + 16 * piece1 < end_b ? base1 + eb : kOut;
+        const uint32_t o2 = eb + 16 * piece2 < end_b ? base2 + eb : kOut;
+        c[0] = __builtin_amdgcn_raw_buffer_load_b128(wr, int(o1), 0, kAuxStream);
+        c[1] = __builtin_amdgcn_raw_buffer_load_b128(wr, int(o2), 0, kAuxStream);
+    };
+    u4 ring[P][2];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        issue(ring[j], E0 + j);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- 4. Metadata to LDS (waits only for the metadata loads). ----
+#pragma unroll
+    for (int u = 0; u < kMetaUnits; ++u) {
+        const uint32_t f = tid + u * nthr;
+        if (f < units) {
+            const uint32_t rl = f / units_per_row;
+            const uint32_t gu = f - rl * units_per_row;
+            uint32_t *dst = ldsM + (rl * Gp + gu * UE) * MW;
+            if constexpr (MB == 4) {
+                dst[0] = mv_s[u];
+                dst[1] = mv_b[u];
+            } else if constexpr (PAIRS) {
+                dst[0] = __builtin_amdgcn_perm(mv_b[u], mv_s[u], 0x05040100u);
+                dst[1] = __builtin_amdgcn_perm(mv_b[u], mv_s[u], 0x07060302u);
+            } else {
+                dst[0] = (mv_s[u] & 0xFFFFu) | (mv_b[u] << 16);
+            }
+        }
+    }
+
+    // ---- 5. x as MFMA A operands: hi/lo f16 with a power-of-two scale per
+    // (quant group, RHS) taken from the group's max |x|, the group sums of x
+    // and the epilogue factors 2^(CODE_EXP + e). ----
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const uint32_t it = tid + i * nthr;
+        if (i > 0 && it >= items) break;  // whole 16-lane blocks are in or out
+        const int m = it & 3;
+        const int g = (it >> 2) & 3;
+        const uint32_t tt = it >> 4;
+        const int t = int(tt % B);
+        const uint32_t Tl = tt / B;
+        float psum = 0.f, mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            psum += xv[i][j];
+            mx = fmaxf(mx, fabsf(xv[i][j]));
+        }
+#pragma unroll
+        for (int o = 1; o < GROUP / 8; o <<= 1) {
+            psum += __shfl_xor(psum, o);
+            mx = fmaxf(mx, __shfl_xor(mx, o));
+        }
+        const uint32_t mb = __float_as_uint(mx);
+        int e = 0;
+        if (mb != 0u && mb < 0x7F800000u) {
+            e = int(mb >> 23) - 127 - 14;  // max * 2^-e in [2^14, 2^15) for normal max
+            e = e < -100 ? -100 : (e > 100 ? 100 : e);
+        }
+        const float sc = __uint_as_float(uint32_t(127 - e) << 23);
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            _Float16 h[2], l[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const float v = xv[i][k_of<BITS>(2 * e2 + q)] * sc;
+                h[q] = static_cast<_Float16>(v);
+                l[q] = static_cast<_Float16>(v - static_cast<float>(h[q]));
+            }
+            hw[e2] = uint32_t(__builtin_bit_cast(uint16_t, h[0])) |
+                     (uint32_t(__builtin_bit_cast(uint16_t, h[1])) << 16);
+            lw[e2] = uint32_t(__builtin_bit_cast(uint16_t, l[0])) |
+                     (uint32_t(__builtin_bit_cast(uint16_t, l[1])) << 16);
+        }
+        if (it < items) {
+            u4 *dst = ldsA + ((Tl * 4 + m) * 4 + g) * (2 * B) + 2 * t;
+            dst[0] = u4{hw[0], hw[1], hw[2], hw[3]};
+            dst[1] = u4{lw[0], lw[1], lw[2], lw[3]};
+            if ((lane & (GROUP / 8 - 1)) == 0) {
+                float *q = reinterpret_cast<float *>(ldsSx + (Tl * NGM + (32 * g) / GROUP) * (HALF / 2) + t / 2);
+                q[t & 1] = psum;
+                q[2 + (t & 1)] = __uint_as_float(uint32_t(127 + kCodeExp<BITS> + e) << 23);
+            }
+        }
+    }
+    if constexpr (HALF > B) {  // slots of absent RHS: zero sums and factors
+        const uint32_t pads = nT * NGM * (HALF - B);
+        for (uint32_t it = tid; it < pads; it += nthr) {
+            const uint32_t blk = it / (HALF - B);
+            const uint32_t t = B + it % (HALF - B);
+            float *q = reinterpret_cast<float *>(ldsSx + blk * (HALF / 2) + t / 2);
+            q[t & 1] = 0.f;
+            q[2 + (t & 1)] = 0.f;
+        }
+    }
+    lds_barrier();
+
+    // ---- 6. Per-lane constants of the A operand and the D epilogue. ----
+    // A lane (slot i = r, chunk g = lg): non-zero when the slot's group is the
+    // chunk's group and the slot's RHS exists; other lanes keep zeros.
+    const int a_slot = r % SLOTS;
+    const bool a_ok = (r / SLOTS) == (32 * lg) / GROUP && a_slot < 2 * B;
+    const uint32_t a_idx = uint32_t(lg) * (2 * B) + uint32_t(a_ok ? a_slot : 0);
+    // D lane (row r, slots 4*lg .. 4*lg+3): group gD, RHS t0 (hi, lo), t0+1.
+    const int gD = (4 * lg) / SLOTS;
+    const int t0 = ((4 * lg) % SLOTS) / 2;
+    const uint32_t m_idx = (uint32_t(wave) * 16 + r) * Gp + uint32_t(gD);
+
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    h8 a[4] = {h8{}, h8{}, h8{}, h8{}};
+    auto compute = [&](const u4 (&c)[NLD], uint32_t Tl) {
+        h8 bq[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) bq[m] = unpack<BITS>(c, m);
+        float sv, bv;
+        if constexpr (MB == 4) {
+            const uint2 mm = *reinterpret_cast<const uint2 *>(ldsM + (m_idx + Tl * NGM) * 2);
+            sv = __uint_as_float(mm.x);
+            bv = __uint_as_float(mm.y);
+        } else {
+            const uint32_t mm = ldsM[m_idx + Tl * NGM];
+            sv = meta_lo<META>(mm);
+            bv = meta_hi<META>(mm);
+        }
+        if (a_ok) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) a[m] = __builtin_bit_cast(h8, ldsA[(Tl * 4 + m) * (8 * B) + a_idx]);
+        }
+        const float4 sx = ldsSx[(Tl * NGM + gD) * (HALF / 2) + t0 / 2];
+        f4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], bq[m], d, 0, 0, 0);
+        const float s0 = sv * sx.z, s1 = sv * sx.w;
+        acc[0] = __builtin_fmaf(s0, d[0], acc[0]);
+        acc[1] = __builtin_fmaf(s0, d[1], acc[1]);
+        acc[2] = __builtin_fmaf(s1, d[2], acc[2]);
+        acc[3] = __builtin_fmaf(s1, d[3], acc[3]);
+        acc[0] = __builtin_fmaf(bv, sx.x, acc[0]);
+        acc[2] = __builtin_fmaf(bv, sx.y, acc[2]);
+    };
+
+    // Swap the pieces of lanes r and r^8 (DPP row rotate by 8 inside each
+    // 16-lane row): afterwards kept = piece kp and got = piece sp of row r.
+    auto exchange = [&](const u4 (&c)[2], u4 &kept, u4 &got) {
+        u4 send;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            kept[d] = lo_half ? c[0][d] : c[1][d];
+            send[d] = lo_half ? c[1][d] : c[0][d];
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) got[d] = uint32_t(__builtin_amdgcn_mov_dpp(int(send[d]), 0x128, 0xF, 0xF, false));
+    };
+
+    // ---- 7. Stream the K range. Loads are issued unconditionally (past the
+    // range they read zeros and move no data), so the ring registers never
+    // merge across branches and each entry waits only for its own loads. ----
+    const uint32_t nE = (nT + TPE - 1) / TPE;
+    for (uint32_t base = 0; base < nE; base += P) {
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            const uint32_t E = base + j;
+            if (E < nE) {
+                u4 kept, got;
+                exchange(ring[j], kept, got);
+                if constexpr (BITS == 4) {
+                    const u4 c0[1] = {kept};
+                    compute(c0, E * 2);
+                    if (E * 2 + 1 < nT) {
+                        const u4 c1[1] = {got};
+                        compute(c1, E * 2 + 1);
+                    }
+                } else {
+                    const u4 c[2] = {kept, got};
+                    compute(c, E);
+                }
+            }
+            issue(ring[j], E0 + E + P);
+        }
+    }
+
+    // ---- 8. Combine hi/lo slots and quant groups; write y or a partial. ----
+    float v0 = acc[0] + acc[1];
+    float v1 = acc[2] + acc[3];
+    if constexpr (NGM == 4) {
+        v0 += __shfl_xor(v0, 16);
+        v1 += __shfl_xor(v1, 16);
+    }
+    if constexpr (NGM >= 2) {
+        v0 += __shfl_xor(v0, 32);
+        v1 += __shfl_xor(v1, 32);
+    }
+    constexpr int WRITERS = 4 / NGM;  // lane groups holding distinct RHS pairs
+    const bool writer = lg < WRITERS && row_ok;
+    if (p.ns == 1) {
+        if (writer) {
+            if (t0 < B) p.y[size_t(t0) * p.rows + row] = v0;
+            if (t0 + 1 < B) p.y[size_t(t0 + 1) * p.rows + row] = v1;
+        }
+        return;
+    }
+    // Split K: publish this split's partial sums; the last workgroup of the
+    // band to arrive adds the ns partials in split order.
+    float *part = p.partial + size_t(split) * B * p.rows;
+    if (writer) {
+        if (t0 < B) __hip_atomic_store(part + size_t(t0) * p.rows + row, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t0 + 1 < B)
+            __hip_atomic_store(part + size_t(t0 + 1) * p.rows + row, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    vmem_order();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&p.counters[band], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *ldsLast = prev == p.ns - 1 ? 1 : 0;
+    }
+    __syncthreads();
+    if (*ldsLast == 0) return;
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const uint32_t band_rows = RT * 16;
+    for (uint32_t i = tid; i < band_rows * B; i += nthr) {
+        const uint32_t t = i / band_rows;
+        const uint32_t rr = band_row0 + i % band_rows;
+        if (rr >= p.rows) continue;
+        // All ns loads in flight at once, then added in split order.
+        float pv[kMaxSplits];
+        const float *pp = p.partial + size_t(t) * p.rows + rr;
+        const size_t stride = size_t(B) * p.rows;
+#pragma unroll
+        for (uint32_t k = 0; k < kMaxSplits; ++k) {
+            pv[k] = k < p.ns ? __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+            pp += stride;
+        }
+        float v = pv[0];
+#pragma unroll
+        for (uint32_t k = 1; k < kMaxSplits; ++k) v += pv[k];
+        p.y[size_t(t) * p.rows + rr] = v;
+    }
+    if (tid == 0) __hip_atomic_store(&p.counters[band], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int BITS, int META, int GROUP, int B, bool PAIRS>
+hipError_t launch_b(const MfmaParams &p, uint32_t rt, size_t lds, hipStream_t stream) {
+    constexpr int P = 4;
+    auto kernel = affine_mfma_kernel<BITS, META, GROUP, B, P, PAIRS>;
+    static size_t configured = 0;
+    if (lds > 65536 && lds > configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess) return e;
+        configured = lds;
+    }
+    hipLaunchKernelGGL(kernel, dim3(p.nbands * p.ns), dim3(rt * 64), lds, stream, p);
+    return hipGetLastError();
+}
+
+template <int BITS, int META, int GROUP, int B>
+hipError_t launch_pairs(const MfmaParams &p, bool pairs, uint32_t rt, size_t lds, hipStream_t stream) {
+    if constexpr (META != 0) {
+        if (pairs) return launch_b<BITS, META, GROUP, B, true>(p, rt, lds, stream);
+    }
+    return launch_b<BITS, META, GROUP, B, false>(p, rt, lds, stream);
+}
+
+template <int BITS, int META, int GROUP>
+hipError_t launch_group(const MfmaParams &p, uint32_t batch, bool pairs, uint32_t rt, size_t lds,
+                        hipStream_t stream) {
+    constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
+    switch (batch) {
+        case 1: return launch_pairs<BITS, META, GROUP, 1>(p, pairs, rt, lds, stream);
+        case 2: return launch_pairs<BITS, META, GROUP, 2>(p, pairs, rt, lds, stream);
+        case 3:
+            if constexpr (MAXB >= 3) return launch_pairs<BITS, META, GROUP, 3>(p, pairs, rt, lds, stream);
+            break;
+        case 4:
+            if constexpr (MAXB >= 4) return launch_pairs<BITS, META, GROUP, 4>(p, pairs, rt, lds, stream);
+            break;
+        default: break;
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int BITS, int META>
+hipError_t launch_meta(const MfmaParams &p, uint32_t group, uint32_t batch, bool pairs, uint32_t rt,
+                       size_t lds, hipStream_t stream) {
+    switch (group) {
+        case 32: return launch_group<BITS, META, 32>(p, batch, pairs, rt, lds, stream);
+        case 64: return launch_group<BITS, META, 64>(p, batch, pairs, rt, lds, stream);
+        case 128: return launch_group<BITS, META, 128>(p, batch, pairs, rt, lds, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+size_t mfma_lds_bytes(uint32_t tps, uint32_t ngm, uint32_t batch, uint32_t rt, bool f32_meta) {
+    const size_t gp = ((size_t(tps) * ngm + 1) | 1);
+    return size_t(tps) * (4 * 4 * 2 * batch * 16 + 64) + size_t(rt) * 16 * gp * 4 * (f32_meta ? 2 : 1) + 16;
+}
+
+MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
+    MfmaPlan pl;
+    if (!affine_mfma_supported(a)) return pl;
+    const uint32_t ngm = kTileK / a.group;
+    const uint32_t row_tiles = (a.rows + 15) / 16;
+    const uint32_t tiles = (a.cols + kTileK - 1) / kTileK;
+    const bool f32_meta = a.meta == Meta::F32;
+    pl.rt = row_tiles < uint32_t(kMaxRt) ? row_tiles : uint32_t(kMaxRt);
+    pl.nbands = (row_tiles + pl.rt - 1) / pl.rt;
+    // Paired (32-bit) metadata loads need every row's run to start on an even
+    // entry: even groups per row and an even number of groups per split.
+    const bool pairs_ok = !f32_meta && (a.cols / a.group) % 2 == 0;
+    // Per-thread staging bounds: x slices (tps * B <= 4 * kItems * rt) and
+    // metadata loads (tps * NGM <= 4 * kMetaUnits * entries per load).
+    const uint32_t cap_x = 4u * kItems * pl.rt / a.batch;
+    // K splits: aim for about ten waves per CU with equal K ranges. Score =
+    // |log(waves/target)| plus twice the log of the split imbalance.
+    const uint32_t cus = lim.num_cus > 0 ? uint32_t(lim.num_cus) : 256u;
+    const double target = 10.0 * cus;
+    double best = 1e30;
+    const uint32_t tpe = 8 / a.bits;  // K tiles per 128-byte load entry
+    for (uint32_t ns = 1; ns <= tiles && ns <= kMaxSplits; ++ns) {
+        uint32_t tps = (tiles + ns - 1) / ns;
+        tps = (tps + tpe - 1) / tpe * tpe;  // splits start on an entry
+        const uint32_t eff = (tiles + tps - 1) / tps;
+        const bool pairs = pairs_ok && (tps * ngm) % 2 == 0;
+        const uint32_t cap_m = 4u * kMetaUnits * (pairs ? 2u : 1u) / ngm;
+        if (tps > cap_x || tps > cap_m || eff != ns) continue;
+        if (mfma_lds_bytes(tps, ngm, a.batch, pl.rt, f32_meta) > lim.max_lds_per_block) continue;
+        const double waves = double(pl.nbands) * pl.rt * eff;
+        const double score = std::fabs(std::log(waves / target)) +
+                             2.0 * std::log(double(tps) * eff / double(tiles));
+        if (score < best - 1e-9) {
+            best = score;
+            pl.tps = tps;
+            pl.ns = eff;
+            pl.pairs = pairs;
+        }
+    }
+    if (pl.ns == 0) {
+        pl.rt = 0;
+        return pl;
+    }
+    pl.tiles = tiles;
+    pl.lds = mfma_lds_bytes(pl.tps, ngm, a.batch, pl.rt, f32_meta);
+    return pl;
+}
+
+bool affine_mfma_supported(const AffineArgs &a) {
+    if (a.bits != 4 && a.bits != 8) return false;
+    if (a.group != 32 && a.group != 64 && a.group != 128) return false;
+    const uint32_t maxb = (16 / (kTileK / a.group)) / 2;
+    if (a.batch < 1 || a.batch > maxb) return false;
+    if (a.cols % 32 != 0 || a.cols % a.group != 0) return false;
+    if ((reinterpret_cast<uintptr_t>(a.w) & 15) != 0) return false;
+    const uint64_t w_bytes = uint64_t(a.rows) * a.cols * a.bits / 8;
+    const uint64_t m_bytes = uint64_t(a.rows) * (a.cols / a.group) * (a.meta == Meta::F32 ? 4 : 2);
+    return w_bytes < (1ull << 31) && m_bytes < (1ull << 31);
+}
+
+size_t affine_mfma_workspace(const MfmaPlan &pl, const AffineArgs &a) {
+    if (pl.ns <= 1) return 0;
+    return size_t(pl.ns) * a.batch * a.rows * sizeof(float);
+}
+
+hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *partial,
+                              uint32_t *counters, hipStream_t stream) {
+    MfmaParams p;
+    p.w = a.w;
+    p.s = a.s;
+    p.b = a.b;
+    p.x = a.x;
+    p.y = a.y;
+    p.partial = partial;
+    p.counters = counters;
+    p.rows = a.rows;
+    p.cols = a.cols;
+    p.w_bytes = uint32_t(uint64_t(a.rows) * a.cols * a.bits / 8);
+    p.m_bytes = uint32_t(uint64_t(a.rows) * (a.cols / a.group) * (a.meta == Meta::F32 ? 4 : 2));
+    p.nbands = pl.nbands;
+    p.ns = pl.ns;
+    p.tiles = pl.tiles;
+    p.tps = pl.tps;
+    const int meta = static_cast<int>(a.meta);
+    if (a.bits == 4) {
+        if (meta == 0) return launch_meta<4, 0>(p, a.group, a.batch, false, pl.rt, pl.lds, stream);
+        if (meta == 1) return launch_meta<4, 1>(p, a.group, a.batch, pl.pairs, pl.rt, pl.lds, stream);
+        return launch_meta<4, 2>(p, a.group, a.batch, pl.pairs, pl.rt, pl.lds, stream);
+    }
+    if (meta == 0) return launch_meta<8, 0>(p, a.group, a.batch, false, pl.rt, pl.lds, stream);
+    if (meta == 1) return launch_meta<8, 1>(p, a.group, a.batch, pl.pairs, pl.rt, pl.lds, stream);
+    return launch_meta<8, 2>(p, a.group, a.batch, pl.pairs, pl.rt, pl.lds, stream);
+}
+
+}  // namespace qmr

@@ -50,6 +50,26 @@ hipError_t launch_dense_f16(const uint16_t *w, const float *x, float *y, uint32_
                             uint32_t cols, uint32_t batch, hipStream_t stream);
 hipError_t launch_embed_f16(const uint16_t *w, uint32_t row, uint32_t cols, float *y,
                             hipStream_t stream);
+// Streaming GEMV / small block on the matrix cores (batch 1..4; Q4/Q8;
+// group 32/64/128 with 2*batch <= 16*group/128). See affine_mfma.hip.
+struct MfmaPlan {
+    uint32_t rt = 0;      // waves (16-row tiles) per workgroup; 0 = unsupported
+    uint32_t nbands = 0;  // row bands
+    uint32_t ns = 0;      // K splits across workgroups
+    uint32_t tiles = 0;   // 128-column K tiles
+    uint32_t tps = 0;     // K tiles per split
+    bool pairs = false;   // 16-bit metadata staged with 32-bit loads
+    size_t lds = 0;       // dynamic LDS bytes per workgroup
+};
+bool affine_mfma_supported(const AffineArgs &a);
+MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim);
+// Workspace bytes the plan needs for cross-workgroup partial sums (0 if none).
+size_t affine_mfma_workspace(const MfmaPlan &pl, const AffineArgs &a);
+// `partial` holds affine_mfma_workspace bytes; `counters` holds pl.nbands
+// zeroed u32 (the kernel returns them to zero).
+hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *partial,
+                              uint32_t *counters, hipStream_t stream);
+
 // Wide block on MFMA (Q4/g64, batch up to 256).
 hipError_t launch_wide_mfma(const AffineArgs &a, const DeviceLimits &lim, hipStream_t stream);
 bool wide_mfma_supported(const AffineArgs &a);

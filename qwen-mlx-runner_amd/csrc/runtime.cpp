@@ -31,6 +31,12 @@ struct qmr_device {
     uint64_t metadata_saved_bytes = 0;
     qmr::GemvPlan forced_plan;  // testing/tuning hook; {0,0} = planner
     std::string last_kernel;    // selected reference pipeline label
+    // Workspace of the matrix-core kernel's cross-workgroup reduction:
+    // partial sums and per-band arrival counters (kept zero between launches).
+    float *ws_partial = nullptr;
+    size_t ws_partial_bytes = 0;
+    uint32_t *ws_counters = nullptr;
+    size_t ws_counter_count = 0;
 };
 
 struct qmr_buffer {
@@ -98,6 +104,45 @@ size_t pipeline_max_threads(const char *label) {
     return 1024;
 }
 
+// Grow the device workspace (synchronising the stream before an old buffer
+// is freed, since queued launches may still use it).
+void ensure_workspace(qmr_device *dev, size_t partial_bytes, size_t counters) {
+    if (partial_bytes > dev->ws_partial_bytes) {
+        check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+        if (dev->ws_partial) hipFree(dev->ws_partial);
+        dev->ws_partial = nullptr;
+        dev->ws_partial_bytes = 0;
+        size_t n = partial_bytes < (size_t(1) << 20) ? (size_t(1) << 20) : partial_bytes;
+        check_hip(hipMalloc(&dev->ws_partial, n), "hipMalloc (workspace)");
+        dev->ws_partial_bytes = n;
+    }
+    if (counters > dev->ws_counter_count) {
+        check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+        if (dev->ws_counters) hipFree(dev->ws_counters);
+        dev->ws_counters = nullptr;
+        dev->ws_counter_count = 0;
+        size_t n = counters < 4096 ? 4096 : counters;
+        check_hip(hipMalloc(&dev->ws_counters, n * sizeof(uint32_t)), "hipMalloc (counters)");
+        check_hip(hipMemset(dev->ws_counters, 0, n * sizeof(uint32_t)), "hipMemset (counters)");
+        dev->ws_counter_count = n;
+    }
+}
+
+// One packed-affine product of at most four RHS: the matrix-core streaming
+// kernel where it supports the format, else the vector-ALU kernels. A forced
+// plan (testing hook) of rr > 0 or rr == -1 selects the vector-ALU tilings.
+hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
+    const qmr::GemvPlan f = dev->forced_plan;
+    if ((f.rr == 0 || f.rr == -2) && qmr::affine_mfma_supported(a)) {
+        const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, dev->limits);
+        if (pl.rt > 0) {
+            ensure_workspace(dev, qmr::affine_mfma_workspace(pl, a), pl.nbands);
+            return qmr::launch_affine_mfma(a, pl, dev->ws_partial, dev->ws_counters, dev->stream);
+        }
+    }
+    return qmr::launch_affine_gemv(a, f.rr == -2 ? qmr::GemvPlan{} : f, dev->limits, dev->stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -160,6 +205,8 @@ void qmr_device_close(qmr_device *device) {
         hipStreamSynchronize(device->stream);
         hipStreamDestroy(device->stream);
     }
+    if (device->ws_partial) hipFree(device->ws_partial);
+    if (device->ws_counters) hipFree(device->ws_counters);
     delete device;
 }
 
@@ -529,12 +576,12 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                     sub.batch = a.batch - t0 < 4 ? a.batch - t0 : 4;
                     sub.x = a.x + size_t(t0) * a.cols;
                     sub.y = a.y + size_t(t0) * a.rows;
-                    e = qmr::launch_affine_gemv(sub, dev->forced_plan, dev->limits, dev->stream);
+                    e = launch_product(dev, sub);
                 }
             } else if (dev->reference || !fast_group) {
                 e = qmr::launch_affine_generic(a, dev->stream);
             } else {
-                e = qmr::launch_affine_gemv(a, dev->forced_plan, dev->limits, dev->stream);
+                e = launch_product(dev, a);
             }
         }
         check_hip(e, "kernel launch");
@@ -625,7 +672,19 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
         a.bits = bits;
         a.group = 64;
         a.batch = batch;
-        const qmr::GemvPlan p = qmr::plan_affine_gemv(a, device->forced_plan, device->limits);
+        a.meta = qmr::Meta::BF16;
+        const qmr::GemvPlan f = device->forced_plan;
+        if ((f.rr == 0 || f.rr == -2) && qmr::affine_mfma_supported(a)) {
+            const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, device->limits);
+            if (pl.rt > 0) {
+                // Matrix-core kernel: rr = -2, ks = K splits across workgroups.
+                if (rr) *rr = -2;
+                if (ks) *ks = int(pl.ns);
+                return QMR_OK;
+            }
+        }
+        const qmr::GemvPlan p = qmr::plan_affine_gemv(a, f.rr == -2 ? qmr::GemvPlan{} : f,
+                                                      device->limits);
         if (rr) *rr = p.rr;
         if (ks) *ks = p.ks;
         return QMR_OK;

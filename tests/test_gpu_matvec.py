@@ -120,7 +120,7 @@ def test_bf16_dispatch_is_unavailable_in_reference_mode(gpus):
         gpu.dispatch("matmul_affine", [w, m, m, x, y], [1, 512, 4, 64, 1])
 
 
-PLANS = [(-1, 0), (1, 1), (2, 1), (4, 1), (5, 2), (2, 2)]
+PLANS = [(-2, 0), (-1, 0), (1, 1), (2, 1), (4, 1), (5, 2), (2, 2)]
 
 
 @pytest.mark.parametrize("rr,ks", PLANS)
