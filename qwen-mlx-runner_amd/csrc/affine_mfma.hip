@@ -61,6 +61,8 @@ namespace qmr {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
@@ -69,9 +71,9 @@ constexpr uint32_t kOut = 0x80000000u;  // buffer offset past every range: loads
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 constexpr int kAuxStream = 2;           // nt: streaming weights
 constexpr int kMaxRt = 8;
-constexpr int kItems = 2;       // staged x slices per thread: tps * B * 16 <= kItems * 64 * rt
-constexpr int kMetaUnits = 5;   // staged metadata loads per thread: ceil(tps*NGM/UE) <= 4 * kMetaUnits
-constexpr uint32_t kMaxSplits = 16;  // K splits across workgroups
+constexpr int kItems = 1;       // staged x slices per thread: tps * B * 16 <= kItems * 64 * rt
+constexpr int kMetaUnits = 2;   // staged metadata loads per thread: ceil(tps*NGM/UE) <= 4 * kMetaUnits
+constexpr uint32_t kMaxSplits = 32;  // K splits across workgroups
 
 struct MfmaParams {
     const uint32_t *w;
@@ -84,6 +86,7 @@ struct MfmaParams {
     uint32_t rows, cols;
     uint32_t w_bytes, m_bytes;  // extents of the code and metadata views
     uint32_t nbands, ns, tiles, tps;
+    uint32_t x16;  // x view is 16-byte aligned
 };
 
 template <int META>
@@ -219,9 +222,14 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     const uint32_t m_pitch = p.cols / GROUP;
     const uint32_t units_per_row = (G + UE - 1) / UE;
     const uint32_t units = RT * 16 * units_per_row;
+    // Loads are issued only by waves that have work (a wave-uniform test), so
+    // idle lanes do not queue memory instructions ahead of the weight ring.
+    const uint32_t wave_base = __builtin_amdgcn_readfirstlane(uint32_t(tid) & ~63u);
     uint32_t mv_s[kMetaUnits], mv_b[kMetaUnits];
 #pragma unroll
     for (int u = 0; u < kMetaUnits; ++u) {
+        mv_s[u] = mv_b[u] = 0u;
+        if (wave_base + u * nthr >= units) continue;
         const uint32_t f = tid + u * nthr;
         const uint32_t rl = f / units_per_row;
         const uint32_t gu = f - rl * units_per_row;
@@ -239,15 +247,33 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     // MFMA m): 8 consecutive columns; the GROUP/8 items of one quant group sit
     // in consecutive lanes. ----
     const uint32_t items = nT * B * 16;
+    // x is read through a buffer view; slices past cols (a K tail) or past
+    // the item count are sent to kOut and read as zeros.
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(p.x), 0, int(uint32_t(B) * p.cols * 4u), kRsrcWord3);
     float xv[kItems][8];
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
+        if (wave_base + i * nthr >= items) continue;
         const uint32_t it = tid + i * nthr;
         const uint32_t tt = it >> 4;
         const uint32_t k = (T0 + tt / B) * kTileK + 32u * ((it >> 2) & 3) + 8u * (it & 3);
-        const float *xs = p.x + size_t(tt % B) * p.cols;
+        const uint32_t xo = (it < items && k < p.cols) ? ((tt % B) * p.cols + k) * 4u : kOut;
+        if (p.x16) {
+            const u4 a = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo), 0, 0);
+            const u4 b = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo + 16u), 0, 0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xv[i][j] = (it < items && k + j < p.cols) ? xs[k + j] : 0.f;
+            for (int j = 0; j < 4; ++j) {
+                xv[i][j] = __uint_as_float(a[j]);
+                xv[i][4 + j] = __uint_as_float(b[j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                xv[i][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, int(xo + 4u * j), 0, 0));
+        }
     }
 
     // ---- 3. The first P entries of codes, requested in ring order. ----
@@ -339,17 +365,14 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
-            _Float16 h[2], l[2];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const float v = xv[i][k_of<BITS>(2 * e2 + q)] * sc;
-                h[q] = static_cast<_Float16>(v);
-                l[q] = static_cast<_Float16>(v - static_cast<float>(h[q]));
-            }
-            hw[e2] = uint32_t(__builtin_bit_cast(uint16_t, h[0])) |
-                     (uint32_t(__builtin_bit_cast(uint16_t, h[1])) << 16);
-            lw[e2] = uint32_t(__builtin_bit_cast(uint16_t, l[0])) |
-                     (uint32_t(__builtin_bit_cast(uint16_t, l[1])) << 16);
+            // Packed round-to-nearest conversions (v_cvt_pk_f16_f32).
+            const float v0 = xv[i][k_of<BITS>(2 * e2)] * sc;
+            const float v1 = xv[i][k_of<BITS>(2 * e2 + 1)] * sc;
+            const h2 hh = __builtin_convertvector(f2{v0, v1}, h2);
+            const h2 ll = __builtin_convertvector(
+                f2{v0 - static_cast<float>(hh.x), v1 - static_cast<float>(hh.y)}, h2);
+            hw[e2] = __builtin_bit_cast(uint32_t, hh);
+            lw[e2] = __builtin_bit_cast(uint32_t, ll);
         }
         if (it < items) {
             u4 *dst = ldsA + ((Tl * 4 + m) * 4 + g) * (2 * B) + 2 * t;
@@ -520,7 +543,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
 
 template <int BITS, int META, int GROUP, int B, bool PAIRS>
 hipError_t launch_b(const MfmaParams &p, uint32_t rt, size_t lds, hipStream_t stream) {
-    constexpr int P = 4;
+    constexpr int P = 2;
     auto kernel = affine_mfma_kernel<BITS, META, GROUP, B, P, PAIRS>;
     static size_t configured = 0;
     if (lds > 65536 && lds > configured) {
@@ -592,10 +615,12 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
     // Per-thread staging bounds: x slices (tps * B <= 4 * kItems * rt) and
     // metadata loads (tps * NGM <= 4 * kMetaUnits * entries per load).
     const uint32_t cap_x = 4u * kItems * pl.rt / a.batch;
-    // K splits: aim for about ten waves per CU with equal K ranges. Score =
-    // |log(waves/target)| plus twice the log of the split imbalance.
+    // K splits: aim for about twenty waves per CU (short K ranges stream
+    // best here: every wave's whole range is requested within two ring
+    // refills) with equal K ranges. Score = |log(waves/target)| plus twice
+    // the log of the split imbalance.
     const uint32_t cus = lim.num_cus > 0 ? uint32_t(lim.num_cus) : 256u;
-    const double target = 10.0 * cus;
+    const double target = 20.0 * cus;
     double best = 1e30;
     const uint32_t tpe = 8 / a.bits;  // K tiles per 128-byte load entry
     for (uint32_t ns = 1; ns <= tiles && ns <= kMaxSplits; ++ns) {
@@ -660,6 +685,7 @@ hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *pa
     p.ns = pl.ns;
     p.tiles = pl.tiles;
     p.tps = pl.tps;
+    p.x16 = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 ? 1u : 0u;
     const int meta = static_cast<int>(a.meta);
     if (a.bits == 4) {
         if (meta == 0) return launch_meta<4, 0>(p, a.group, a.batch, false, pl.rt, pl.lds, stream);
