@@ -119,19 +119,42 @@ def cpu_baseline(m: synth.PackedMatrix, budget_s: float) -> dict:
     med = statistics.median(times)
     nbytes = synth.algorithmic_bytes(m, 1)
     return {
-        "value": round(med * 1e6, 1), "unit": "us/matrix", "cores": threads, "kind": "port",
+        "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
         "sample": (f"FP64 oracle (oracle/qmr_oracle.c, per-weight dequantise then FP64 "
-                   f"accumulate) on the full {m.rows}x{m.cols} Q4/g64 BF16 B=1 matrix, "
-                   f"median of {reps} runs on {threads} threads"),
-        "gbps": round(nbytes / med / 1e9, 2),
+                   f"accumulate) on the full {m.rows}x{m.cols} Q4/g64 BF16 B=1 matrix "
+                   f"({nbytes} algorithmic bytes), median of {reps} runs on {threads} threads"),
+        "us_per_matrix": round(med * 1e6, 1),
         "single_thread_us": round(single * 1e6, 1),
         "fp32_accumulate_us": round(f32 * 1e6, 1),
         "cpu_model": model, "host_cores_visible": cores,
     }
 
 
+def copy_calibration(gpu: qmr.Gpu, mib: int, launches: int) -> None:
+    """Plain copies of a known size (copy_f32: `mib` MiB read and `mib` MiB
+    written per launch, over two buffer pairs) for calibrating rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters in the same process as the metric
+    kernel. Not part of the timed metric."""
+    n = mib * (1 << 20) // 4
+    pairs = [(gpu.upload_f32(np.ones(n, np.float32)), gpu.alloc_f32(n)) for _ in range(2)]
+    cmd = gpu.begin()
+    for k in range(launches):
+        src, dst = pairs[k % 2]
+        cmd.encode("copy_f32", [src, dst], [n], n, 128)
+    cmd.finish()
+    cmd.release()
+    log(f"bench: copy calibration, {launches} x copy_f32 of {mib} MiB")
+    del pairs
+
+
+def hip_kernel(plan) -> str:
+    """The HIP kernel family the planner picked (plan[0] == -2: matrix cores)."""
+    return "affine_mfma_kernel" if plan[0] == -2 else "affine_gemv_kernel"
+
+
 def load_traffic(tag: str):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by its copy_f32 calibration)."""
     p = ROOT / "profiles" / "pmc_traffic.json"
     if not p.exists():
         return None
@@ -152,6 +175,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-metric", action="store_true",
                     help="time only the 5120x17408 shapes (for profiling runs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first run plain copies of MIB MiB (counter calibration for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the hot path is "
@@ -162,6 +187,8 @@ def main() -> int:
 
     gpu = qmr.Gpu("aligned")
     log(f"bench: device {gpu.name()}, steps={args.steps} warmup={args.warmup} copies={args.copies}")
+    if args.copy_calibration:
+        copy_calibration(gpu, args.copy_calibration, 8)
     shapes = [("down", synth.MLP_SHAPES["down"])]
     if not args.only_metric:
         shapes.append(("gate_up", synth.MLP_SHAPES["gate_up"]))
@@ -185,7 +212,9 @@ def main() -> int:
             nbytes = synth.algorithmic_bytes(m, batch)
             q = np.quantile(durs, [0.1, 0.5, 0.9])
             r = {
-                "shape": f"{rows}x{cols}", "tag": tag, "batch": batch, "kernel": gpu.last_kernel(),
+                "shape": f"{rows}x{cols}", "tag": tag, "batch": batch,
+                "reference_pipeline": gpu.last_kernel(),
+                "kernel": hip_kernel(gpu.gemv_plan(rows, cols, 4, batch)),
                 "plan": list(gpu.gemv_plan(rows, cols, 4, batch)),
                 "us_mean": round(mean_ms * 1e3, 3),
                 "us_bracketed_p10_p50_p90": [round(v * 1e3, 3) for v in q],
@@ -207,7 +236,8 @@ def main() -> int:
     if not args.no_cpu and metric_matrix is not None:
         log("bench: CPU baseline (FP64 oracle)")
         cpu = cpu_baseline(metric_matrix, args.cpu_seconds)
-        log(f"bench:   CPU {cpu['value']} us/matrix on {cpu['cores']} threads")
+        log(f"bench:   CPU {cpu['us_per_matrix']} us/matrix ({cpu['value']} GB/s) on "
+            f"{cpu['cores']} threads")
     line = {
         "metric": METRIC,
         "value": head["gbps"],
@@ -235,7 +265,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": head["frac_peak"],
             "traffic": load_traffic("down_b1"),
-            "kernel": head["kernel"],
+            "kernel": hip_kernel(head["plan"]),
         },
         "cpu_baseline": cpu,
         "results": results,

@@ -118,7 +118,7 @@ int qmr_command_begin(qmr_device *device, qmr_command **out);
 /* DispatchEncoder::encode / encode_offsets (src/gpu.rs:120-141):
  * `name` is a reference kernel name (matvec_affine, matvec_affine_bf16,
  * matmul_affine, matmul_affine_bf16, embed_affine, embed_affine_bf16,
- * matvec_f16, matmul_f16, embed_f16) or one of this library's additions
+ * matvec_f16, matmul_f16, embed_f16, copy_f32) or one of this library's additions
  * (matmul_affine_wide[_bf16], see below). `offsets` may be NULL (all zero) or
  * hold one 4-byte-aligned byte offset per buffer. `params`, `threads` and
  * `group_size` follow dispatch_layout (src/gpu.rs:1041-1294). */

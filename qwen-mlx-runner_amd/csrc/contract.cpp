@@ -82,7 +82,9 @@ bool ranges_overlap(size_t a, size_t a_len, size_t b, size_t b_len) {
 // F16-metadata and wide-block names.
 Layout dispatch_layout(const std::string &name, const uint32_t *p, size_t np) {
     size_t count;
-    if (name == "matvec_f16" || name == "embed_f16") {
+    if (name == "copy_f32") {
+        count = 1;
+    } else if (name == "matvec_f16" || name == "embed_f16") {
         count = 2;
     } else if (name == "matvec_affine" || name == "embed_affine" || name == "matvec_affine_bf16" ||
                name == "embed_affine_bf16" || name == "matvec_affine_f16meta" ||
@@ -116,6 +118,14 @@ Layout dispatch_layout(const std::string &name, const uint32_t *p, size_t np) {
     const Meta meta = meta_of_name(name);
     const size_t meta_bytes_per = meta == Meta::F32 ? 4 : 2;
     Layout out;
+
+    // src/gpu.rs:1173-1176: copy_f32 [n] -> two views of n floats, n threads.
+    if (name == "copy_f32") {
+        positive({0});
+        out.sizes = {f(product({n(0)})), f(product({n(0)}))};
+        out.threads = n(0);
+        return out;
+    }
 
     if (starts_with(name, "matvec_") || starts_with(name, "embed_")) {
         positive({1});

@@ -50,6 +50,8 @@ hipError_t launch_dense_f16(const uint16_t *w, const float *x, float *y, uint32_
                             uint32_t cols, uint32_t batch, hipStream_t stream);
 hipError_t launch_embed_f16(const uint16_t *w, uint32_t row, uint32_t cols, float *y,
                             hipStream_t stream);
+// y[i] = x[i] for i < n (x == y allowed only as the identical view).
+hipError_t launch_copy_f32(const float *x, float *y, uint32_t n, int num_cus, hipStream_t stream);
 // Streaming GEMV / small block on the matrix cores (batch 1..4; Q4/Q8;
 // group 32/64/128 with 2*batch <= 16*group/128). See affine_mfma.hip.
 struct MfmaPlan {

@@ -5,7 +5,9 @@
 //   - row dequantisation (embed_affine[_bf16], kernels/qwen.metal:73-77,
 //     kernels/affine_bf16.metal:162-174), bit-exact RN32(q*s + b);
 //   - dense F16 matvec / blocks / embedding (kernels/qwen.metal:48-57,69-72,
-//     kernels/matmul_block.metal:213-248).
+//     kernels/matmul_block.metal:213-248);
+//   - copy_f32 (kernels/matmul_block.metal:315-318), a streaming copy that is
+//     also the known-size kernel HBM byte counters are calibrated against.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -135,6 +137,40 @@ hipError_t launch_embed_f16(const uint16_t *w, uint32_t row, uint32_t cols, floa
                             hipStream_t stream) {
     hipLaunchKernelGGL(embed_f16_kernel, dim3((cols + 255) / 256), dim3(256), 0, stream, w, row,
                        cols, y);
+    return hipGetLastError();
+}
+
+namespace {
+
+typedef uint32_t copy_u4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes per lane per step, grid-stride; the scalar tail covers n % 4 and
+// views that are not 16-byte aligned. An identical source and destination
+// view (allowed by the dispatch contract) rewrites each element in place.
+__global__ __launch_bounds__(256) void copy_f32_kernel(const float *__restrict__ x,
+                                                       float *__restrict__ y, uint32_t n,
+                                                       uint32_t vec) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t nv = vec ? n / 4 : 0;
+    const copy_u4 *xv = reinterpret_cast<const copy_u4 *>(x);
+    copy_u4 *yv = reinterpret_cast<copy_u4 *>(y);
+    for (uint32_t i = tid; i < nv; i += stride) __builtin_nontemporal_store(xv[i], yv + i);
+    for (uint32_t i = nv * 4 + tid; i < n; i += stride) y[i] = x[i];
+}
+
+}  // namespace
+
+hipError_t launch_copy_f32(const float *x, float *y, uint32_t n, int num_cus,
+                           hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    const bool vec = (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16 == 0;
+    const uint64_t items = vec ? (uint64_t(n) + 3) / 4 : n;
+    const uint64_t want = (items + 255) / 256;
+    const uint64_t cap = uint64_t(num_cus > 0 ? num_cus : 256) * 16;
+    const uint32_t blocks = uint32_t(want < cap ? want : cap);
+    hipLaunchKernelGGL(copy_f32_kernel, dim3(blocks), dim3(256), 0, stream, x, y, n,
+                       uint32_t(vec));
     return hipGetLastError();
 }
 

@@ -481,12 +481,15 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                 throw Error{e.code, name + ": buffer " + std::to_string(i) + ": " + e.message};
             }
         }
-        // A matrix-block output is never an input (src/gpu.rs:658-672).
-        if (qmr::starts_with(name, "matmul_")) {
+        // A matrix-block output is never an input; a copy's views are
+        // disjoint or identical (src/gpu.rs:658-672).
+        if (qmr::starts_with(name, "matmul_") || name == "copy_f32") {
             const size_t out = nbuffers - 1;
             for (size_t i = 0; i < out; ++i) {
                 if (buffers[i] == buffers[out]) {
-                    ensure(!qmr::ranges_overlap(off(i), layout.sizes[i], off(out), layout.sizes[out]),
+                    const bool identical_copy = name == "copy_f32" && off(i) == off(out);
+                    ensure(identical_copy ||
+                               !qmr::ranges_overlap(off(i), layout.sizes[i], off(out), layout.sizes[out]),
                            name + ": output overlaps input buffer " + std::to_string(i));
                 }
             }
@@ -543,6 +546,10 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
             e = qmr::launch_embed_affine(reinterpret_cast<const uint32_t *>(ptr(0)), ptr(1), ptr(2),
                                          meta, params[0], params[1], params[2], params[3],
                                          reinterpret_cast<float *>(ptr(3)), dev->stream);
+        } else if (name == "copy_f32") {
+            e = qmr::launch_copy_f32(reinterpret_cast<const float *>(ptr(0)),
+                                     reinterpret_cast<float *>(ptr(1)), params[0], dev->limits.num_cus,
+                                     dev->stream);
         } else if (name == "embed_f16") {
             e = qmr::launch_embed_f16(reinterpret_cast<const uint16_t *>(ptr(0)), params[0],
                                       params[1], reinterpret_cast<float *>(ptr(1)), dev->stream);

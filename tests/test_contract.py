@@ -119,6 +119,8 @@ def test_batch_dispatch_layout_sizes_all_rhs_and_rejects_invalid_batches():
     for p in ([3, 127, 4, 64, 2], [3, 256, 4, 256, 2], [3, 128, 2, 64, 2], [U32_MAX, 128, 4, 64, 4]):
         err(qmr.dispatch_layout, "matmul_affine", p)
     err(qmr.dispatch_layout, "matmul_f16", [1, U32_MAX, 4])
+    assert qmr.dispatch_layout("copy_f32", [7]) == ([28, 28], 7)
+    err(qmr.dispatch_layout, "copy_f32", [0])
 
 
 # src/gpu.rs:1568-1582

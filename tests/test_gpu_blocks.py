@@ -72,6 +72,12 @@ def test_dense_blocks_keep_guard_values(gpu):
                 got = gpu.read_f32(yb, batch * rows + 2)
                 assert got[0] == 12345.0 and got[batch * rows + 1] == 12345.0
                 block_close(got[1:batch * rows + 1], want[:batch * rows], f"dense {rows}x{cols} B{batch}")
+                # tests/batch_matrix.rs:149-166: the block copied at an offset, guards kept.
+                cb = gpu.upload_f32(np.full(batch * rows + 2, 54321.0))
+                gpu.dispatch("copy_f32", [yb, cb], [batch * rows], offsets=[4, 4])
+                copied = gpu.read_f32(cb, batch * rows + 2)
+                assert copied[0] == 54321.0 and copied[batch * rows + 1] == 54321.0
+                assert np.array_equal(copied[1:batch * rows + 1], got[1:batch * rows + 1])
 
 
 def test_offset_dispatch_rejects_bounds_and_unsafe_aliases(gpu):
@@ -81,6 +87,13 @@ def test_offset_dispatch_rejects_bounds_and_unsafe_aliases(gpu):
     s = gpu.upload_f32(np.ones(32))
     b = gpu.upload_f32(np.ones(32))
     cmd = gpu.begin()
+    # tests/batch_matrix.rs:176-191: copies need disjoint or identical views.
+    for offs in ([0], [2, 0], [0, 2**63], [4, 4]):
+        with pytest.raises(qmr.QmrError):
+            cmd.encode("copy_f32", [inp, out], [1028], 1028, 128, offs)
+    with pytest.raises(qmr.QmrError, match="overlaps input buffer 0"):
+        cmd.encode("copy_f32", [inp, inp], [32], 32, 128, [0, 4])
+    cmd.encode("copy_f32", [inp, inp], [32], 32, 128, [4, 4])
     # Misaligned and out-of-range views are rejected before anything is enqueued.
     for offs in ([0, 0, 0, 2, 0], [0, 0, 0, 0, 2**63], [0, 0, 0, 4, 4100]):
         with pytest.raises(qmr.QmrError):
