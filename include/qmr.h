@@ -173,12 +173,22 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  */
 
 /* ---- Testing and tuning hooks (no counterpart in the reference). ---- */
-/* Force the GEMV tiling: rr = -1 selects the streaming single-RHS kernel
- * (blocks then use the planner's row-slot tiling); rr > 0 with ks > 0
- * selects the row-slot kernel with `rr` rows per slot and a K-split of
- * `ks`; 0,0 = planner. Pairs that are not compiled fall back to the planner. */
+/* Force the GEMV kernel and tiling; 0,0 = planner (split-K matrix-core
+ * kernel where supported, else the vector-ALU kernels).
+ *   rr = -3: row-owning matrix-core kernel (opt-in); ks = j*10000 + rt*100 + kw
+ *            pins its workgroup shape (rt row tiles x kw K waves) and, when
+ *            j > 0, the entries per wave per staged chunk; 0 = its planner.
+ *   rr = -2: split-K matrix-core kernel (ks ignored).
+ *   rr = -1: the vector-ALU streaming single-RHS kernel (blocks then use
+ *            the row-slot tiling).
+ *   rr > 0 with ks > 0: the vector-ALU row-slot kernel with `rr` rows per
+ *            slot and a K-split of `ks`.
+ * Shapes a forced kernel does not support fall back to the next one; pairs
+ * that are not compiled fall back to the planner. */
 int qmr_set_gemv_plan(qmr_device *device, int rr, int ks);
-/* The plan the GEMV launcher uses for a shape (honours a forced plan). */
+/* The plan the GEMV launcher uses for a shape with group 64 and BF16
+ * metadata (honours a forced plan), in the encoding of qmr_set_gemv_plan;
+ * the split-K kernel reports rr = -2 with ks = its K splits. */
 int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32_t bits,
                   uint32_t batch, int *rr, int *ks);
 /* Reference pipeline label selected by the last successful qmr_encode. */

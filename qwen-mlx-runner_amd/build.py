@@ -29,6 +29,7 @@ SOURCES = [
     ("runtime.cpp", ["-x", "hip"]),
     ("affine_gemv.hip", ["-x", "hip"]),
     ("affine_mfma.hip", ["-x", "hip"]),
+    ("affine_rows.hip", ["-x", "hip"]),
     ("misc_kernels.hip", ["-x", "hip"]),
     ("wide_mfma.hip", ["-x", "hip"]),
 ]

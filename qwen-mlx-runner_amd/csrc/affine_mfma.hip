@@ -25,20 +25,7 @@
 // encoding) and 2^e (activation scale) are restored exactly in the FP32
 // epilogue.
 //
-// Operand placement (16x16x32 f16: A row i = lane%16, B column j = lane%16,
-// both taking K chunk lane/16; D[i][j] lives in lane j + 16*(i/4), element
-// i%4):
-//   B operand = codes: lane (r, g) holds 8 codes of weight row r (one u32
-//     word for Q4, two for Q8) from K chunk g.
-//   A operand = activations: row i is a "slot" (group gamma, RHS t, part
-//     hi/lo); it is non-zero only on the K chunks that belong to quant group
-//     gamma, so one MFMA keeps the partial dots of different quant groups in
-//     different D rows and the per-group scale can be applied afterwards.
-// A tile is 16 rows x 128 K: each lane loads 16 B (Q4) or 32 B (Q8) of codes
-// with one or two 128-bit buffer loads, plus its group's scale and bias; four
-// MFMAs consume the tile. Lane (r, g) of D holds the four slots of one quant
-// group and row r, i.e. exactly the group whose scale/bias that lane loaded,
-// so the epilogue is four FMAs for the scales and two for the biases.
+// Operands, code encoding and the tile product are in mfma_common.hpp.
 //
 // Work decomposition. A wave owns one 16-row tile and a contiguous range of
 // K tiles; a workgroup holds RT waves (RT row tiles) over the same K range
@@ -47,8 +34,8 @@
 // nbands x ns workgroups (row bands x K splits). With ns > 1 each workgroup
 // writes its partial sums to a workspace; the last workgroup of a band to
 // finish (an atomic counter) adds the ns partials in split order and writes
-// y, so results do not depend on timing. Each lane keeps P tiles of loads in
-// flight in a register ring; the first P tiles are requested before x is
+// y, so results do not depend on timing. Each lane keeps P entries of loads
+// in flight in a register ring; the first P entries are requested before x is
 // staged.
 #include <hip/hip_runtime.h>
 
@@ -56,20 +43,13 @@
 #include <cstdint>
 
 #include "kernels.hpp"
+#include "mfma_common.hpp"
 
 namespace qmr {
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f2 __attribute__((ext_vector_type(2)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+using namespace mfma;
 
-constexpr int kTileK = 128;             // K per tile
-constexpr uint32_t kOut = 0x80000000u;  // buffer offset past every range: loads return 0
-constexpr uint32_t kRsrcWord3 = 0x00020000u;
-constexpr int kAuxStream = 2;           // nt: streaming weights
 constexpr int kMaxRt = 8;
 constexpr int kItems = 1;       // staged x slices per thread: tps * B * 16 <= kItems * 64 * rt
 constexpr int kMetaUnits = 2;   // staged metadata loads per thread: ceil(tps*NGM/UE) <= 4 * kMetaUnits
@@ -88,80 +68,6 @@ struct MfmaParams {
     uint32_t nbands, ns, tiles, tps;
     uint32_t x16;  // x view is 16-byte aligned
 };
-
-template <int META>
-__device__ __forceinline__ float meta_f32(uint32_t v) {
-    if constexpr (META == 0) {
-        return __uint_as_float(v);
-    } else if constexpr (META == 1) {
-        return __uint_as_float(v << 16);
-    } else {
-        return float(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v)));
-    }
-}
-
-// Code encoding. A code is placed inside a 16-bit half so that the half is an
-// IEEE f16 subnormal of value q * 2^-CODE_EXP. The matrix core rounds
-// products of the smallest subnormals (codes in bits 0-3, q * 2^-24) with a
-// biased error near 2^-22 of the dot product, while codes at bits 4-7 (Q4,
-// q * 2^-20) or bits 2-9 (Q8, q * 2^-22) are as accurate as normal f16
-// operands (about 2^-27 relative to the sum of |products|, unbiased); bits
-// 10-14 are the exponent, so no higher placement is linear in q.
-//   Q4 word -> halves [q0, q4 | q1, q5 | q2, q6 | q3, q7] * 2^-20
-//   Q8 words w0,w1 -> [b0, b2 | b1, b3 | b4, b6 | b5, b7] * 2^-22
-// k_of(e) is the column (within the 8-column chunk) of half e.
-template <int BITS>
-constexpr int kCodeExp = BITS == 4 ? 20 : 22;
-
-template <int BITS>
-__device__ __forceinline__ int k_of(int e) {
-    if constexpr (BITS == 4) {
-        constexpr int k[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-        return k[e];
-    } else {
-        constexpr int k[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-        return k[e];
-    }
-}
-
-template <int BITS>
-__device__ __forceinline__ h8 unpack(const u4 (&c)[BITS / 4], int m) {
-    u4 v;
-    if constexpr (BITS == 4) {
-        const uint32_t wd = c[0][m];
-        v[0] = (wd << 4) & 0x00F000F0u;
-        v[1] = wd & 0x00F000F0u;
-        v[2] = (wd >> 4) & 0x00F000F0u;
-        v[3] = (wd >> 8) & 0x00F000F0u;
-    } else {
-        const uint32_t w0 = c[(2 * m) >> 2][(2 * m) & 3];
-        const uint32_t w1 = c[(2 * m + 1) >> 2][(2 * m + 1) & 3];
-        v[0] = (w0 << 2) & 0x03FC03FCu;
-        v[1] = (w0 >> 6) & 0x03FC03FCu;
-        v[2] = (w1 << 2) & 0x03FC03FCu;
-        v[3] = (w1 >> 6) & 0x03FC03FCu;
-    }
-    return __builtin_bit_cast(h8, v);
-}
-
-// Workgroup barrier ordering LDS only: outstanding global loads (the weight
-// ring) stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-template <int META>
-__device__ __forceinline__ float meta_lo(uint32_t v) {  // entry packed as s | b << 16
-    if constexpr (META == 1) return __uint_as_float(v << 16);
-    return float(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v & 0xFFFFu)));
-}
-template <int META>
-__device__ __forceinline__ float meta_hi(uint32_t v) {
-    if constexpr (META == 1) return __uint_as_float(v & 0xFFFF0000u);
-    return float(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v >> 16)));
-}
 
 // Order this wave's earlier global writes before what follows, without the
 // device-scope fence (which writes back and invalidates the L2). Visibility
@@ -209,6 +115,8 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     uint32_t *ldsM = reinterpret_cast<uint32_t *>(ldsSx + size_t(p.tps) * NGM * (HALF / 2));
     // ldsM [RT*16 rows][Gp] entries: s | b << 16 (16-bit) or (s, b) as two words
     int *ldsLast = reinterpret_cast<int *>(ldsM + size_t(RT) * 16 * Gp * MW);
+
+    const uint32_t tile0 = band_row0 + wave * 16;
 
     const __amdgpu_buffer_rsrc_t wr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(p.w), 0, int(p.w_bytes), kRsrcWord3);
@@ -258,22 +166,8 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
         if (wave_base + i * nthr >= items) continue;
         const uint32_t it = tid + i * nthr;
-        const uint32_t tt = it >> 4;
-        const uint32_t k = (T0 + tt / B) * kTileK + 32u * ((it >> 2) & 3) + 8u * (it & 3);
-        const uint32_t xo = (it < items && k < p.cols) ? ((tt % B) * p.cols + k) * 4u : kOut;
-        if (p.x16) {
-            const u4 a = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo), 0, 0);
-            const u4 b = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo + 16u), 0, 0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                xv[i][j] = __uint_as_float(a[j]);
-                xv[i][4 + j] = __uint_as_float(b[j]);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                xv[i][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, int(xo + 4u * j), 0, 0));
-        }
+        load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), T0 * kTileK + item_col<B>(it), p.cols, it < items,
+                p.x16 != 0);
     }
 
     // ---- 3. The first P entries of codes, requested in ring order. ----
@@ -291,7 +185,6 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     const uint32_t piece1 = lo_half ? kp : sp;  // load 1 (rows 0-7)
     const uint32_t piece2 = lo_half ? sp : kp;  // load 2 (rows 8-15)
     const uint32_t row_bytes = p.cols / 32 * LANE_BYTES;
-    const uint32_t tile0 = band_row0 + wave * 16;
     const uint32_t base1 = (tile0 + (r & 7)) * row_bytes + 16 * piece1;
     const uint32_t base2 = (tile0 + 8 + (r & 7)) * row_bytes + 16 * piece2;
     // Bytes of each row this split may read: min(row end, split end).
@@ -311,6 +204,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         issue(ring[j], E0 + j);
         __builtin_amdgcn_sched_barrier(0);
     }
+
 
     // ---- 4. Metadata to LDS (waits only for the metadata loads). ----
 #pragma unroll
@@ -332,113 +226,28 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         }
     }
 
-    // ---- 5. x as MFMA A operands: hi/lo f16 with a power-of-two scale per
-    // (quant group, RHS) taken from the group's max |x|, the group sums of x
-    // and the epilogue factors 2^(CODE_EXP + e). ----
+    // ---- 5. x as MFMA A operands (hi/lo f16, group sums, epilogue factors). ----
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
         const uint32_t it = tid + i * nthr;
         if (i > 0 && it >= items) break;  // whole 16-lane blocks are in or out
-        const int m = it & 3;
-        const int g = (it >> 2) & 3;
-        const uint32_t tt = it >> 4;
-        const int t = int(tt % B);
-        const uint32_t Tl = tt / B;
-        float psum = 0.f, mx = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            psum += xv[i][j];
-            mx = fmaxf(mx, fabsf(xv[i][j]));
-        }
-#pragma unroll
-        for (int o = 1; o < GROUP / 8; o <<= 1) {
-            psum += __shfl_xor(psum, o);
-            mx = fmaxf(mx, __shfl_xor(mx, o));
-        }
-        const uint32_t mb = __float_as_uint(mx);
-        int e = 0;
-        if (mb != 0u && mb < 0x7F800000u) {
-            e = int(mb >> 23) - 127 - 14;  // max * 2^-e in [2^14, 2^15) for normal max
-            e = e < -100 ? -100 : (e > 100 ? 100 : e);
-        }
-        const float sc = __uint_as_float(uint32_t(127 - e) << 23);
-        uint32_t hw[4], lw[4];
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-            // Packed round-to-nearest conversions (v_cvt_pk_f16_f32).
-            const float v0 = xv[i][k_of<BITS>(2 * e2)] * sc;
-            const float v1 = xv[i][k_of<BITS>(2 * e2 + 1)] * sc;
-            const h2 hh = __builtin_convertvector(f2{v0, v1}, h2);
-            const h2 ll = __builtin_convertvector(
-                f2{v0 - static_cast<float>(hh.x), v1 - static_cast<float>(hh.y)}, h2);
-            hw[e2] = __builtin_bit_cast(uint32_t, hh);
-            lw[e2] = __builtin_bit_cast(uint32_t, ll);
-        }
-        if (it < items) {
-            u4 *dst = ldsA + ((Tl * 4 + m) * 4 + g) * (2 * B) + 2 * t;
-            dst[0] = u4{hw[0], hw[1], hw[2], hw[3]};
-            dst[1] = u4{lw[0], lw[1], lw[2], lw[3]};
-            if ((lane & (GROUP / 8 - 1)) == 0) {
-                float *q = reinterpret_cast<float *>(ldsSx + (Tl * NGM + (32 * g) / GROUP) * (HALF / 2) + t / 2);
-                q[t & 1] = psum;
-                q[2 + (t & 1)] = __uint_as_float(uint32_t(127 + kCodeExp<BITS> + e) << 23);
-            }
-        }
+        stage_x_item<BITS, GROUP, B>(xv[i], it, it < items, lane, ldsA, ldsSx);
     }
-    if constexpr (HALF > B) {  // slots of absent RHS: zero sums and factors
-        const uint32_t pads = nT * NGM * (HALF - B);
-        for (uint32_t it = tid; it < pads; it += nthr) {
-            const uint32_t blk = it / (HALF - B);
-            const uint32_t t = B + it % (HALF - B);
-            float *q = reinterpret_cast<float *>(ldsSx + blk * (HALF / 2) + t / 2);
-            q[t & 1] = 0.f;
-            q[2 + (t & 1)] = 0.f;
-        }
-    }
+    stage_x_pads<GROUP, B>(nT, tid, nthr, ldsSx);
     lds_barrier();
 
     // ---- 6. Per-lane constants of the A operand and the D epilogue. ----
-    // A lane (slot i = r, chunk g = lg): non-zero when the slot's group is the
-    // chunk's group and the slot's RHS exists; other lanes keep zeros.
-    const int a_slot = r % SLOTS;
-    const bool a_ok = (r / SLOTS) == (32 * lg) / GROUP && a_slot < 2 * B;
-    const uint32_t a_idx = uint32_t(lg) * (2 * B) + uint32_t(a_ok ? a_slot : 0);
-    // D lane (row r, slots 4*lg .. 4*lg+3): group gD, RHS t0 (hi, lo), t0+1.
-    const int gD = (4 * lg) / SLOTS;
-    const int t0 = ((4 * lg) % SLOTS) / 2;
-    const uint32_t m_idx = (uint32_t(wave) * 16 + r) * Gp + uint32_t(gD);
+    const LaneMap<GROUP, B> L(lane);
+    const int t0 = L.t0;
+    const uint32_t m_idx = (uint32_t(wave) * 16 + r) * Gp + uint32_t(L.gD);
 
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     h8 a[4] = {h8{}, h8{}, h8{}, h8{}};
     auto compute = [&](const u4 (&c)[NLD], uint32_t Tl) {
-        h8 bq[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) bq[m] = unpack<BITS>(c, m);
         float sv, bv;
-        if constexpr (MB == 4) {
-            const uint2 mm = *reinterpret_cast<const uint2 *>(ldsM + (m_idx + Tl * NGM) * 2);
-            sv = __uint_as_float(mm.x);
-            bv = __uint_as_float(mm.y);
-        } else {
-            const uint32_t mm = ldsM[m_idx + Tl * NGM];
-            sv = meta_lo<META>(mm);
-            bv = meta_hi<META>(mm);
-        }
-        if (a_ok) {
-#pragma unroll
-            for (int m = 0; m < 4; ++m) a[m] = __builtin_bit_cast(h8, ldsA[(Tl * 4 + m) * (8 * B) + a_idx]);
-        }
-        const float4 sx = ldsSx[(Tl * NGM + gD) * (HALF / 2) + t0 / 2];
-        f4 d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int m = 0; m < 4; ++m) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], bq[m], d, 0, 0, 0);
-        const float s0 = sv * sx.z, s1 = sv * sx.w;
-        acc[0] = __builtin_fmaf(s0, d[0], acc[0]);
-        acc[1] = __builtin_fmaf(s0, d[1], acc[1]);
-        acc[2] = __builtin_fmaf(s1, d[2], acc[2]);
-        acc[3] = __builtin_fmaf(s1, d[3], acc[3]);
-        acc[0] = __builtin_fmaf(bv, sx.x, acc[0]);
-        acc[2] = __builtin_fmaf(bv, sx.y, acc[2]);
+        meta_entry<META>(ldsM + (m_idx + Tl * NGM) * MW, sv, bv);
+        const float4 sx = ldsSx[(Tl * NGM + L.gD) * (HALF / 2) + t0 / 2];
+        tile_product<BITS, META, GROUP, B>(c, L, ldsA + Tl * 4 * (8 * B), sv, bv, sx, a, acc);
     };
 
     // Swap the pieces of lanes r and r^8 (DPP row rotate by 8 inside each
@@ -482,16 +291,8 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     }
 
     // ---- 8. Combine hi/lo slots and quant groups; write y or a partial. ----
-    float v0 = acc[0] + acc[1];
-    float v1 = acc[2] + acc[3];
-    if constexpr (NGM == 4) {
-        v0 += __shfl_xor(v0, 16);
-        v1 += __shfl_xor(v1, 16);
-    }
-    if constexpr (NGM >= 2) {
-        v0 += __shfl_xor(v0, 32);
-        v1 += __shfl_xor(v1, 32);
-    }
+    float v0, v1;
+    combine_slots<GROUP>(acc, v0, v1);
     constexpr int WRITERS = 4 / NGM;  // lane groups holding distinct RHS pairs
     const bool writer = lg < WRITERS && row_ok;
     if (p.ns == 1) {

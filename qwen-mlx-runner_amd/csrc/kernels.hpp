@@ -1,5 +1,6 @@
 // Launch interface between the host runtime (runtime.cpp) and the HIP
-// kernels (affine_gemv.hip, misc_kernels.hip, wide_mfma.hip).
+// kernels (affine_rows.hip, affine_mfma.hip, affine_gemv.hip,
+// misc_kernels.hip, wide_mfma.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -71,6 +72,26 @@ size_t affine_mfma_workspace(const MfmaPlan &pl, const AffineArgs &a);
 // zeroed u32 (the kernel returns them to zero).
 hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *partial,
                               uint32_t *counters, hipStream_t stream);
+
+// Streaming GEMV / small block on the matrix cores with every workgroup
+// owning whole rows (no cross-workgroup reduction). See affine_rows.hip.
+struct RowsPlan {
+    uint32_t rt = 0;         // 16-row tiles per workgroup; 0 = unsupported
+    uint32_t kw = 0;         // K waves per tile
+    uint32_t j = 0;          // entries per wave per staged chunk
+    uint32_t nbands = 0;     // workgroups
+    uint32_t n_entries = 0;  // 128-byte entries per row
+    uint32_t n_chunks = 0;   // ceil(n_entries / (kw * j))
+    bool pairs = false;      // 16-bit metadata staged with 32-bit loads
+    size_t stage_bytes = 0;  // one LDS staging buffer
+    size_t lds = 0;          // dynamic LDS bytes per workgroup
+};
+bool affine_rows_supported(const AffineArgs &a);
+// force_rt/force_kw (both nonzero) pin the workgroup shape and force_j the
+// chunk depth; zeros leave the choice to the planner.
+RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_rt = 0,
+                          uint32_t force_kw = 0, uint32_t force_j = 0);
+hipError_t launch_affine_rows(const AffineArgs &a, const RowsPlan &pl, hipStream_t stream);
 
 // Wide block on MFMA (Q4/g64, batch up to 256).
 hipError_t launch_wide_mfma(const AffineArgs &a, const DeviceLimits &lim, hipStream_t stream);

@@ -29,9 +29,13 @@ struct qmr_device {
     qmr::DeviceLimits limits{};
     size_t compacted_matrices = 0;
     uint64_t metadata_saved_bytes = 0;
-    qmr::GemvPlan forced_plan;  // testing/tuning hook; {0,0} = planner
+    // Testing/tuning hook; {0,0} = planner. rr = -3: row-owning matrix-core
+    // kernel, opt-in (ks = j*10000 + rt*100 + kw; j = 0 or ks = 0 leave the
+    // choice to its planner); rr = -2: split-K matrix-core kernel; rr = -1 or
+    // rr > 0: vector-ALU kernels.
+    qmr::GemvPlan forced_plan;
     std::string last_kernel;    // selected reference pipeline label
-    // Workspace of the matrix-core kernel's cross-workgroup reduction:
+    // Workspace of the split-K matrix-core kernel's cross-workgroup reduction:
     // partial sums and per-band arrival counters (kept zero between launches).
     float *ws_partial = nullptr;
     size_t ws_partial_bytes = 0;
@@ -123,24 +127,39 @@ void ensure_workspace(qmr_device *dev, size_t partial_bytes, size_t counters) {
         dev->ws_counter_count = 0;
         size_t n = counters < 4096 ? 4096 : counters;
         check_hip(hipMalloc(&dev->ws_counters, n * sizeof(uint32_t)), "hipMalloc (counters)");
-        check_hip(hipMemset(dev->ws_counters, 0, n * sizeof(uint32_t)), "hipMemset (counters)");
+        check_hip(hipMemsetAsync(dev->ws_counters, 0, n * sizeof(uint32_t), dev->stream),
+                  "hipMemsetAsync (counters)");
         dev->ws_counter_count = n;
     }
 }
 
-// One packed-affine product of at most four RHS: the matrix-core streaming
+// The row-owning kernel's plan, honouring a forced workgroup shape.
+qmr::RowsPlan forced_rows_plan(const qmr_device *dev, const qmr::AffineArgs &a) {
+    const qmr::GemvPlan f = dev->forced_plan;
+    if (f.rr == -3 && f.ks > 0)
+        return qmr::plan_affine_rows(a, dev->limits, uint32_t(f.ks / 100 % 100), uint32_t(f.ks % 100),
+                                     uint32_t(f.ks / 10000));
+    return qmr::plan_affine_rows(a, dev->limits);
+}
+
+// One packed-affine product of at most four RHS: the split-K matrix-core
 // kernel where it supports the format, else the vector-ALU kernels. A forced
-// plan (testing hook) of rr > 0 or rr == -1 selects the vector-ALU tilings.
+// plan (testing hook) of rr > 0 or rr == -1 selects the vector-ALU tilings,
+// rr == -3 the row-owning matrix-core kernel.
 hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
     const qmr::GemvPlan f = dev->forced_plan;
-    if ((f.rr == 0 || f.rr == -2) && qmr::affine_mfma_supported(a)) {
+    if (f.rr == -3 && qmr::affine_rows_supported(a)) {
+        const qmr::RowsPlan pl = forced_rows_plan(dev, a);
+        if (pl.rt > 0) return qmr::launch_affine_rows(a, pl, dev->stream);
+    }
+    if ((f.rr == 0 || f.rr == -2 || f.rr == -3) && qmr::affine_mfma_supported(a)) {
         const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, dev->limits);
         if (pl.rt > 0) {
             ensure_workspace(dev, qmr::affine_mfma_workspace(pl, a), pl.nbands);
             return qmr::launch_affine_mfma(a, pl, dev->ws_partial, dev->ws_counters, dev->stream);
         }
     }
-    return qmr::launch_affine_gemv(a, f.rr == -2 ? qmr::GemvPlan{} : f, dev->limits, dev->stream);
+    return qmr::launch_affine_gemv(a, f.rr < -1 ? qmr::GemvPlan{} : f, dev->limits, dev->stream);
 }
 
 }  // namespace
@@ -272,10 +291,13 @@ int qmr_buffer_alloc(qmr_device *device, size_t bytes, qmr_buffer **out) {
         check_hip(hipSetDevice(device->ordinal), "hipSetDevice");
         void *p = nullptr;
         check_hip(hipMalloc(&p, n), "hipMalloc");
-        hipError_t e = hipMemset(p, 0, n);
+        // Zeroed on the device stream and waited for, so the fill is ordered
+        // before both later launches and host reads.
+        hipError_t e = hipMemsetAsync(p, 0, n, device->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(device->stream);
         if (e != hipSuccess) {
             hipFree(p);
-            check_hip(e, "hipMemset");
+            check_hip(e, "hipMemsetAsync");
         }
         auto *b = new qmr_buffer();
         b->ordinal = device->ordinal;
@@ -681,7 +703,16 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
         a.batch = batch;
         a.meta = qmr::Meta::BF16;
         const qmr::GemvPlan f = device->forced_plan;
-        if ((f.rr == 0 || f.rr == -2) && qmr::affine_mfma_supported(a)) {
+        if (f.rr == -3 && qmr::affine_rows_supported(a)) {
+            const qmr::RowsPlan pl = forced_rows_plan(device, a);
+            if (pl.rt > 0) {
+                // Row-owning kernel: rr = -3, ks = j*10000 + rt*100 + kw.
+                if (rr) *rr = -3;
+                if (ks) *ks = int(pl.j * 10000 + pl.rt * 100 + pl.kw);
+                return QMR_OK;
+            }
+        }
+        if ((f.rr == 0 || f.rr == -2 || f.rr == -3) && qmr::affine_mfma_supported(a)) {
             const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, device->limits);
             if (pl.rt > 0) {
                 // Matrix-core kernel: rr = -2, ks = K splits across workgroups.
@@ -690,7 +721,7 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
                 return QMR_OK;
             }
         }
-        const qmr::GemvPlan p = qmr::plan_affine_gemv(a, f.rr == -2 ? qmr::GemvPlan{} : f,
+        const qmr::GemvPlan p = qmr::plan_affine_gemv(a, f.rr < -1 ? qmr::GemvPlan{} : f,
                                                       device->limits);
         if (rr) *rr = p.rr;
         if (ks) *ks = p.ks;

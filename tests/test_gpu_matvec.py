@@ -120,7 +120,11 @@ def test_bf16_dispatch_is_unavailable_in_reference_mode(gpus):
         gpu.dispatch("matmul_affine", [w, m, m, x, y], [1, 512, 4, 64, 1])
 
 
-PLANS = [(-2, 0), (-1, 0), (1, 1), (2, 1), (4, 1), (5, 2), (2, 2)]
+# (-3, rt*100 + kw): row-owning matrix-core kernel with a pinned workgroup
+# shape (0 = its planner); (-2, 0): split-K matrix-core kernel; the rest are
+# the vector-ALU tilings.
+PLANS = [(-3, 0), (-3, 102), (-3, 104), (-3, 116), (-3, 204), (-3, 208), (-3, 402), (-3, 801),
+         (-2, 0), (-1, 0), (1, 1), (2, 1), (4, 1), (5, 2), (2, 2)]
 
 
 @pytest.mark.parametrize("rr,ks", PLANS)
@@ -130,7 +134,7 @@ def test_every_compiled_tiling_matches_oracle(gpu, rr, ks):
     code widths, the three metadata types and batches 1..4."""
     gpu.set_gemv_plan(rr, ks)
     try:
-        rng = np.random.default_rng(abs(rr) * 10 + ks + (rr < 0))
+        rng = np.random.default_rng(abs(rr) * 10 + ks % 97 + (rr < 0))
         for bits, meta, rows, cols in [(4, "bf16", 37, 1536), (4, "f32", 41, 64 * 17),
                                        (8, "f16", 23, 1024 + 256), (4, "f16", 3, 5120),
                                        (8, "bf16", 45, 64 * 9)]:
@@ -165,3 +169,63 @@ def test_config0_golden_meets_gate(gpu):
     got = run_affine(gpu, "matvec_affine_bf16", m.w, m.s, m.b, x, 1024, 1024, 4, 64)
     assert gpu.last_kernel() == "matvec_q4_g64_aligned_bf16"
     assert_gate(got, z["y64"], "config 0")
+
+
+SPLIT_SHAPES = [(5120, 17408, 1), (37, 64 * 136, 3), (300, 4096, 2), (64, 32 * 128, 4),
+                (1000, 64 * 30, 1)]
+
+
+def _launch_three(gpu, rows, cols, batch, seed):
+    """Three launches of one product in one command (distinct outputs)."""
+    rng = np.random.default_rng(seed)
+    w = rng.integers(0, 2**32, rows * cols // 8, dtype=np.uint32)
+    sf = rng.uniform(0.002, 0.02, rows * cols // 64).astype(np.float32)
+    bf = (-8 * sf + rng.normal(0, 1e-3, sf.size)).astype(np.float32)
+    s, b = synth.f32_to_bf16_bits(sf), synth.f32_to_bf16_bits(bf)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    wb, sb, bb = gpu.upload_bytes(w), gpu.upload_bytes(s), gpu.upload_bytes(b)
+    xb = gpu.upload_f32(x.ravel())
+    ys = [gpu.alloc_f32(batch * rows) for _ in range(3)]
+    params = [rows, cols, 4, 64, batch]
+    _, threads = qmr.dispatch_layout("matmul_affine_bf16", params)
+    cmd = gpu.begin()
+    for yb in ys:
+        cmd.encode("matmul_affine_bf16", [wb, sb, bb, xb, yb], params, threads, 128)
+    cmd.finish()
+    cmd.release()
+    got = [gpu.read_f32(yb, batch * rows) for yb in ys]
+    want = oracle.matmul_f64(w, s, b, "bf16", x, rows, cols, 4, 64, batch, 8)
+    return got, want
+
+
+@pytest.mark.parametrize("rows,cols,batch", SPLIT_SHAPES)
+def test_split_k_reduction_is_deterministic_across_launches(gpu, rows, cols, batch):
+    """The split-K matrix-core kernel's reduction (the last workgroup of a
+    band to arrive adds the partials in split order): several launches in one
+    command give bit-identical y that meets the gate; row tails included."""
+    gpu.set_gemv_plan(-2, 0)
+    try:
+        plan = gpu.gemv_plan(rows, cols, 4, batch)
+        assert plan[0] == -2 and plan[1] > 1, f"expected a split-K matrix-core plan, got {plan}"
+        got, want = _launch_three(gpu, rows, cols, batch, rows * 7 + batch)
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    for g in got[1:]:
+        assert np.array_equal(g.view(np.uint32), got[0].view(np.uint32)), "launches differ"
+    assert_gate(got[0], want, f"split-K {plan} {rows}x{cols} B{batch}")
+
+
+@pytest.mark.parametrize("rows,cols,batch", SPLIT_SHAPES)
+def test_row_kernel_is_deterministic(gpu, rows, cols, batch):
+    """The row-owning matrix-core kernel (opt-in) under its own planner:
+    repeated launches give bit-identical y that meets the gate."""
+    gpu.set_gemv_plan(-3, 0)
+    try:
+        plan = gpu.gemv_plan(rows, cols, 4, batch)
+        assert plan[0] == -3, f"expected the row-owning kernel, got {plan}"
+        got, want = _launch_three(gpu, rows, cols, batch, rows * 11 + batch)
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    for g in got[1:]:
+        assert np.array_equal(g.view(np.uint32), got[0].view(np.uint32)), "launches differ"
+    assert_gate(got[0], want, f"rows {plan} {rows}x{cols} B{batch}")
