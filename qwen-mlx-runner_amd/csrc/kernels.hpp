@@ -93,9 +93,13 @@ RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                           uint32_t force_kw = 0, uint32_t force_j = 0);
 hipError_t launch_affine_rows(const AffineArgs &a, const RowsPlan &pl, hipStream_t stream);
 
-// Wide block on MFMA (Q4/g64, batch up to 256).
-hipError_t launch_wide_mfma(const AffineArgs &a, const DeviceLimits &lim, hipStream_t stream);
+// Wide block on MFMA (Q4/g64, F32 or BF16 metadata, batch up to 256): a prep
+// launch converts x into per-group images in `workspace` (wide_mfma_workspace
+// bytes), then the contraction launch. See wide_mfma.hip.
 bool wide_mfma_supported(const AffineArgs &a);
+size_t wide_mfma_workspace(const AffineArgs &a);
+hipError_t launch_wide_mfma(const AffineArgs &a, unsigned char *workspace, const DeviceLimits &lim,
+                            hipStream_t stream);
 
 // The plan the GEMV launcher would use (for tests and tuning reports).
 GemvPlan plan_affine_gemv(const AffineArgs &a, GemvPlan forced, const DeviceLimits &lim);

@@ -41,6 +41,9 @@ struct qmr_device {
     size_t ws_partial_bytes = 0;
     uint32_t *ws_counters = nullptr;
     size_t ws_counter_count = 0;
+    // Workspace of the wide-block kernel: the activation images.
+    unsigned char *ws_wide = nullptr;
+    size_t ws_wide_bytes = 0;
 };
 
 struct qmr_buffer {
@@ -225,6 +228,7 @@ void qmr_device_close(qmr_device *device) {
         hipStreamDestroy(device->stream);
     }
     if (device->ws_partial) hipFree(device->ws_partial);
+    if (device->ws_wide) hipFree(device->ws_wide);
     if (device->ws_counters) hipFree(device->ws_counters);
     delete device;
 }
@@ -596,7 +600,16 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
             a.meta = meta;
             const bool fast_group = a.group == 32 || a.group == 64 || a.group == 128;
             if (wide && qmr::wide_mfma_supported(a)) {
-                e = qmr::launch_wide_mfma(a, dev->limits, dev->stream);
+                const size_t need = qmr::wide_mfma_workspace(a);
+                if (need > dev->ws_wide_bytes) {
+                    check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+                    if (dev->ws_wide) hipFree(dev->ws_wide);
+                    dev->ws_wide = nullptr;
+                    dev->ws_wide_bytes = 0;
+                    check_hip(hipMalloc(&dev->ws_wide, need), "hipMalloc (wide workspace)");
+                    dev->ws_wide_bytes = need;
+                }
+                e = qmr::launch_wide_mfma(a, dev->ws_wide, dev->limits, dev->stream);
             } else if (wide) {
                 // Wide blocks outside the MFMA kernel's format run as
                 // successive small blocks of up to four RHS.

@@ -85,8 +85,27 @@ def test_config3_vocabulary_head(gpu):
     check_dequant_rows(gpu, m, [0, rows - 1])
 
 
-def test_config4_wide_block(gpu):
+@pytest.mark.parametrize("batch", [128, 256])
+def test_config4_wide_block(gpu, batch):
     rows, cols = synth.MLP_SHAPES["gate_up"]
     m = synth.q4_bf16_matrix(rows, cols, SEED, tag="gate_up")
     sample = sorted(set(list(range(0, rows, 271)) + [rows - 1]))
-    check(gpu, m, 128, sample, name="matmul_affine_wide_bf16")
+    check(gpu, m, batch, sample, name="matmul_affine_wide_bf16")
+
+
+@pytest.mark.parametrize("rows,cols,batch,meta", [(300, 1024, 100, "bf16"), (128, 512, 64, "f32"),
+                                                  (17, 512, 5, "bf16"), (1000, 2048, 256, "f32"),
+                                                  (250, 1536, 65, "bf16")])
+def test_wide_block_tails_and_metadata(gpu, rows, cols, batch, meta):
+    """Wide blocks at ragged row and column counts (row blocks of 128,
+    column blocks of 64), both wide names, against the FP64 oracle."""
+    rng = np.random.default_rng(rows + batch)
+    w = rng.integers(0, 2**32, rows * cols // 8, dtype=np.uint32)
+    sf = rng.uniform(0.002, 0.02, rows * cols // 64).astype(np.float32)
+    bf = (-8 * sf + rng.normal(0, 1e-3, sf.size)).astype(np.float32)
+    s, b = (synth.f32_to_bf16_bits(sf), synth.f32_to_bf16_bits(bf)) if meta == "bf16" else (sf, bf)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    name = "matmul_affine_wide" + NAME[meta]
+    got = run_affine(gpu, name, w, s, b, x, rows, cols, 4, 64, batch)
+    want = oracle.matmul_f64(w, s, b, meta, x, rows, cols, 4, 64, batch, THREADS)
+    assert_gate(got, want, f"{name} {rows}x{cols} B{batch}")
