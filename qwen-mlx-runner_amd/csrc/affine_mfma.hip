@@ -41,6 +41,9 @@
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
+#include <type_traits>
+#include <vector>
 
 #include "kernels.hpp"
 #include "mfma_common.hpp"
@@ -342,10 +345,11 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     if (tid == 0) __hip_atomic_store(&p.counters[band], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+constexpr int kRing = 2;  // entries in flight per wave
+
 template <int BITS, int META, int GROUP, int B, bool PAIRS>
 hipError_t launch_b(const MfmaParams &p, uint32_t rt, size_t lds, hipStream_t stream) {
-    constexpr int P = 2;
-    auto kernel = affine_mfma_kernel<BITS, META, GROUP, B, P, PAIRS>;
+    auto kernel = affine_mfma_kernel<BITS, META, GROUP, B, kRing, PAIRS>;
     static size_t configured = 0;
     if (lds > 65536 && lds > configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
@@ -394,6 +398,75 @@ hipError_t launch_meta(const MfmaParams &p, uint32_t group, uint32_t batch, bool
     }
 }
 
+// The kernel instance for a format, for occupancy queries.
+template <int BITS, int META, int GROUP>
+const void *instance_group(uint32_t batch, bool pairs) {
+    constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
+    auto pick = [&](auto bconst) -> const void * {
+        constexpr int B = decltype(bconst)::value;
+        if constexpr (META != 0) {
+            if (pairs) return reinterpret_cast<const void *>(affine_mfma_kernel<BITS, META, GROUP, B, kRing, true>);
+        }
+        return reinterpret_cast<const void *>(affine_mfma_kernel<BITS, META, GROUP, B, kRing, false>);
+    };
+    switch (batch) {
+        case 1: return pick(std::integral_constant<int, 1>{});
+        case 2: return pick(std::integral_constant<int, 2>{});
+        case 3:
+            if constexpr (MAXB >= 3) return pick(std::integral_constant<int, 3>{});
+            break;
+        case 4:
+            if constexpr (MAXB >= 4) return pick(std::integral_constant<int, 4>{});
+            break;
+        default: break;
+    }
+    return nullptr;
+}
+
+template <int BITS, int META>
+const void *instance_meta(uint32_t group, uint32_t batch, bool pairs) {
+    switch (group) {
+        case 32: return instance_group<BITS, META, 32>(batch, pairs);
+        case 64: return instance_group<BITS, META, 64>(batch, pairs);
+        case 128: return instance_group<BITS, META, 128>(batch, pairs);
+        default: return nullptr;
+    }
+}
+
+const void *instance(const AffineArgs &a, bool pairs) {
+    const int meta = static_cast<int>(a.meta);
+    if (a.bits == 4) {
+        if (meta == 0) return instance_meta<4, 0>(a.group, a.batch, false);
+        if (meta == 1) return instance_meta<4, 1>(a.group, a.batch, pairs);
+        return instance_meta<4, 2>(a.group, a.batch, pairs);
+    }
+    if (meta == 0) return instance_meta<8, 0>(a.group, a.batch, false);
+    if (meta == 1) return instance_meta<8, 1>(a.group, a.batch, pairs);
+    return instance_meta<8, 2>(a.group, a.batch, pairs);
+}
+
+// Resident workgroups per CU for a kernel instance, block size and dynamic
+// LDS (as the runtime computes it from registers and LDS); cached.
+uint32_t resident_per_cu(const void *kernel, uint32_t threads, size_t lds) {
+    struct Entry {
+        const void *k;
+        uint32_t threads;
+        size_t lds;
+        uint32_t n;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry &e : cache)
+        if (e.k == kernel && e.threads == threads && e.lds == lds) return e.n;
+    int n = 0;
+    if (kernel == nullptr ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, int(threads), lds) != hipSuccess || n < 1)
+        n = 1;
+    cache.push_back(Entry{kernel, threads, lds, uint32_t(n)});
+    return uint32_t(n);
+}
+
 }  // namespace
 
 size_t mfma_lds_bytes(uint32_t tps, uint32_t ngm, uint32_t batch, uint32_t rt, bool f32_meta) {
@@ -418,10 +491,10 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
     const uint32_t cap_x = 4u * kItems * pl.rt / a.batch;
     // K splits: aim for about twenty waves per CU (short K ranges stream
     // best here: every wave's whole range is requested within two ring
-    // refills) with equal K ranges. Score = |log(waves/target)| plus twice
-    // the log of the split imbalance.
+    // refills) with equal K ranges, and never more workgroups than stay
+    // resident at once (a second round would add a whole wave of latency).
+    // Score = |log(waves/target)| plus twice the log of the split imbalance.
     const uint32_t cus = lim.num_cus > 0 ? uint32_t(lim.num_cus) : 256u;
-    const double target = 20.0 * cus;
     double best = 1e30;
     const uint32_t tpe = 8 / a.bits;  // K tiles per 128-byte load entry
     for (uint32_t ns = 1; ns <= tiles && ns <= kMaxSplits; ++ns) {
@@ -431,10 +504,13 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
         const bool pairs = pairs_ok && (tps * ngm) % 2 == 0;
         const uint32_t cap_m = 4u * kMetaUnits * (pairs ? 2u : 1u) / ngm;
         if (tps > cap_x || tps > cap_m || eff != ns) continue;
-        if (mfma_lds_bytes(tps, ngm, a.batch, pl.rt, f32_meta) > lim.max_lds_per_block) continue;
+        const size_t lds = mfma_lds_bytes(tps, ngm, a.batch, pl.rt, f32_meta);
+        if (lds > lim.max_lds_per_block) continue;
+        const uint32_t resident = resident_per_cu(instance(a, pairs), pl.rt * 64, lds) * cus;
+        const double target = std::min(20.0, double(resident / cus) * pl.rt) * cus;
         const double waves = double(pl.nbands) * pl.rt * eff;
-        const double score = std::fabs(std::log(waves / target)) +
-                             2.0 * std::log(double(tps) * eff / double(tiles));
+        double score = std::fabs(std::log(waves / target)) + 2.0 * std::log(double(tps) * eff / double(tiles));
+        if (pl.nbands * eff > resident) score += 10.0 * std::ceil(double(pl.nbands * eff) / resident);
         if (score < best - 1e-9) {
             best = score;
             pl.tps = tps;
