@@ -69,7 +69,6 @@ struct MfmaParams {
     uint32_t rows, cols;
     uint32_t w_bytes, m_bytes;  // extents of the code and metadata views
     uint32_t nbands, ns, tiles, tps;
-    uint32_t x16;  // x view is 16-byte aligned
 };
 
 // Order this wave's earlier global writes before what follows, without the
@@ -169,8 +168,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
         if (wave_base + i * nthr >= items) continue;
         const uint32_t it = tid + i * nthr;
-        load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), T0 * kTileK + item_col<B>(it), p.cols, it < items,
-                p.x16 != 0);
+        load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), T0 * kTileK + item_col<B>(it), p.cols, it < items);
     }
 
     // ---- 3. The first P entries of codes, requested in ring order. ----
@@ -562,7 +560,6 @@ hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *pa
     p.ns = pl.ns;
     p.tiles = pl.tiles;
     p.tps = pl.tps;
-    p.x16 = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 ? 1u : 0u;
     const int meta = static_cast<int>(a.meta);
     if (a.bits == 4) {
         if (meta == 0) return launch_meta<4, 0>(p, a.group, a.batch, false, pl.rt, pl.lds, stream);

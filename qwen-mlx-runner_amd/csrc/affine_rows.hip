@@ -73,7 +73,6 @@ struct RowsParams {
     uint32_t n_entries;         // 128-byte entries per row (the last may be partial)
     uint32_t n_chunks;          // ceil(n_entries / (kw * j))
     uint32_t stage_bytes;       // one LDS staging buffer (16-byte multiple)
-    uint32_t x16;               // x view is 16-byte aligned
 };
 
 template <int BITS, int META, int GROUP, int B, bool PAIRS>
@@ -144,7 +143,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void affine_rows_kernel(RowsParams 
             if (wave_base + i * nthr >= items) continue;
             const uint32_t it = tid + i * nthr;
             load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), c * CT * kTileK + item_col<B>(it), p.cols,
-                    it < items, p.x16 != 0);
+                    it < items);
         }
 #pragma unroll
         for (int u = 0; u < kMUnits; ++u) {
@@ -466,7 +465,6 @@ hipError_t launch_affine_rows(const AffineArgs &a, const RowsPlan &pl, hipStream
     p.n_entries = pl.n_entries;
     p.n_chunks = pl.n_chunks;
     p.stage_bytes = uint32_t(pl.stage_bytes);
-    p.x16 = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 ? 1u : 0u;
     const int meta = static_cast<int>(a.meta);
     if (a.bits == 4) {
         if (meta == 0) return launch_meta<4, 0>(p, a.group, a.batch, false, pl.nbands, pl.lds, stream);

@@ -168,22 +168,20 @@ __device__ __forceinline__ uint32_t item_col(uint32_t it) {
 }
 
 // Loads the 8 columns of x[t] at column k (x view of B rows of cols floats);
-// columns at or past cols, or a dead item, read as zeros.
+// columns at or past cols, or a dead item, read as zeros. Two 128-bit loads
+// whatever the view's alignment: multi-dword buffer loads need only 4-byte
+// alignment, which every buffer offset has. (A runtime choice between load
+// shapes here made the compiler wait for these loads before issuing the
+// weight loads behind them.)
 __device__ __forceinline__ void load_x8(float (&xv)[8], __amdgpu_buffer_rsrc_t xr, uint32_t t,
-                                        uint32_t k, uint32_t cols, bool live, bool x16) {
+                                        uint32_t k, uint32_t cols, bool live) {
     const uint32_t xo = (live && k < cols) ? (t * cols + k) * 4u : kOut;
-    if (x16) {
-        const u4 a = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo), 0, 0);
-        const u4 b = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo + 16u), 0, 0);
+    const u4 a = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo), 0, 0);
+    const u4 b = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo + 16u), 0, 0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            xv[j] = __uint_as_float(a[j]);
-            xv[4 + j] = __uint_as_float(b[j]);
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            xv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, int(xo + 4u * j), 0, 0));
+    for (int j = 0; j < 4; ++j) {
+        xv[j] = __uint_as_float(a[j]);
+        xv[4 + j] = __uint_as_float(b[j]);
     }
 }
 

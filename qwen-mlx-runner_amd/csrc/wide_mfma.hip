@@ -64,7 +64,6 @@ struct WideParams {
     uint32_t rows, cols, n;    // n = RHS count
     uint32_t ncb;              // column blocks
     uint32_t nrb;              // row blocks
-    uint32_t x16;
     uint32_t w_bytes, m_bytes, img_bytes;  // extents of the views
 };
 
@@ -81,8 +80,8 @@ __global__ __launch_bounds__(kPrepThreads) void wide_prep_kernel(WideParams p) {
         const_cast<float *>(p.x), 0, int(p.n * p.cols * 4u), kRsrcWord3);
     float xv[2][8];
     const uint32_t k0 = g * 64 + sg * 16;
-    load_x8(xv[0], xr, t, k0, p.cols, t < p.n, p.x16 != 0);
-    load_x8(xv[1], xr, t, k0 + 8, p.cols, t < p.n, p.x16 != 0);
+    load_x8(xv[0], xr, t, k0, p.cols, t < p.n);
+    load_x8(xv[1], xr, t, k0 + 8, p.cols, t < p.n);
     float sum = 0.f, mx = 0.f;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -407,7 +406,6 @@ hipError_t launch_wide_mfma(const AffineArgs &a, unsigned char *workspace, const
     p.n = a.batch;
     p.ncb = (a.batch + kColBlock - 1) / kColBlock;
     p.nrb = (a.rows + kRowBlock - 1) / kRowBlock;
-    p.x16 = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 ? 1u : 0u;
     p.w_bytes = uint32_t(uint64_t(a.rows) * a.cols / 2);
     p.m_bytes = uint32_t(uint64_t(a.rows) * (a.cols / 64) * (a.meta == Meta::F32 ? 4 : 2));
     p.img_bytes = uint32_t(wide_mfma_workspace(a));

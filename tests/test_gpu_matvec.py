@@ -229,3 +229,36 @@ def test_row_kernel_is_deterministic(gpu, rows, cols, batch):
     for g in got[1:]:
         assert np.array_equal(g.view(np.uint32), got[0].view(np.uint32)), "launches differ"
     assert_gate(got[0], want, f"rows {plan} {rows}x{cols} B{batch}")
+
+
+@pytest.mark.parametrize("rr,name,batch", [(0, "matmul_affine_bf16", 1), (0, "matmul_affine_bf16", 3),
+                                           (-3, "matmul_affine_bf16", 2), (0, "matmul_affine_wide_bf16", 100)])
+def test_matrix_core_kernels_read_x_at_4_byte_offsets(gpu, rr, name, batch):
+    """x (and y) views 4-byte but not 16-byte aligned, as the block contract
+    allows (tests/batch_matrix.rs:176-191; the BF16 matvec names require
+    16-byte aligned input instead), with codes and metadata aligned so the
+    matrix-core kernels (split-K, row-owning, wide) take the product: their
+    x loads are 128-bit loads that need only 4-byte alignment."""
+    rows, cols = 300, 4096
+    rng = np.random.default_rng(batch * 7 + (rr < 0))
+    w = rng.integers(0, 2**32, rows * cols // 8, dtype=np.uint32)
+    sf = rng.uniform(0.002, 0.02, rows * cols // 64).astype(np.float32)
+    bf = (-8 * sf + rng.normal(0, 1e-3, sf.size)).astype(np.float32)
+    s, b = synth.f32_to_bf16_bits(sf), synth.f32_to_bf16_bits(bf)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    want = oracle.matmul_f64(w, s, b, "bf16", x, rows, cols, 4, 64, batch)
+    gpu.set_gemv_plan(rr, 0)
+    try:
+        if batch <= 4:
+            plan = gpu.gemv_plan(rows, cols, 4, batch)
+            assert plan[0] in (-2, -3), f"expected a matrix-core plan, got {plan}"
+        wb, sb, bb = gpu.upload_bytes(w), gpu.upload_bytes(s), gpu.upload_bytes(b)
+        xb = gpu.upload_f32(np.concatenate([[99.0], x.ravel()]).astype(np.float32))
+        yb = gpu.upload_f32(np.full(batch * rows + 2, 12345.0, np.float32))
+        params = [rows, cols, 4, 64] + ([batch] if name.startswith("matmul") else [])
+        gpu.dispatch(name, [wb, sb, bb, xb, yb], params, offsets=[0, 0, 0, 4, 4])
+        got = gpu.read_f32(yb, batch * rows + 2)
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    assert got[0] == 12345.0 and got[batch * rows + 1] == 12345.0
+    assert_gate(got[1:batch * rows + 1], want, f"{name} B{batch} x at a 4-byte offset")
