@@ -19,6 +19,11 @@ events to report the spread.
 
 The CPU baseline times the FP64 oracle (the reference's per-weight
 dequantise-then-accumulate closure, restated in C) on this host.
+
+BASELINE config 4 (the wide block: 17408x5120 Q4/g64 BF16 times 128 and 256
+FP32 columns) is timed the same way and reported under "wide" with its own
+matrix-core roofline (algorithmic FLOP against the dense f16 peak); it is not
+the headline metric.
 """
 from __future__ import annotations
 
@@ -40,6 +45,7 @@ import qmr.synth as synth  # noqa: E402
 
 METRIC = "Q4/g64 GEMV µs + achieved HBM GB/s (% peak), 5120x17408 at B=1 and B=3"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 matrix-core peak
 
 
 def log(msg: str) -> None:
@@ -147,6 +153,40 @@ def copy_calibration(gpu: qmr.Gpu, mib: int, launches: int) -> None:
     del pairs
 
 
+def bench_wide(gpu: qmr.Gpu, args) -> list:
+    """the 17408x5120 Q4/g64 BF16 matrix times 128 and 256
+    FP32 columns (matmul_affine_wide_bf16), 4 rotating weight copies."""
+    rows, cols = synth.MLP_SHAPES["gate_up"]
+    m = synth.q4_bf16_matrix(rows, cols, synth.DEFAULT_SEED, tag="gate_up")
+    mats = [(gpu.upload_bytes(m.w), gpu.upload_bytes(m.s), gpu.upload_bytes(m.b)) for _ in range(4)]
+    out = []
+    for batch in (128, 256):
+        x = synth.activations(cols, batch, synth.DEFAULT_SEED, tag="wide")
+        xb = gpu.upload_f32(x.ravel())
+        ys = [gpu.alloc_f32(batch * rows) for _ in range(len(mats))]
+        bufsets = [[w, s, b, xb, y] for (w, s, b), y in zip(mats, ys)]
+        log(f"bench: wide {rows}x{cols} x {batch} (matmul_affine_wide_bf16)")
+        mean_ms, _, _ = time_kernel(gpu, "matmul_affine_wide_bf16", bufsets, [rows, cols, 4, 64, batch],
+                                    args.wide_steps, 5)
+        flop = 2.0 * rows * cols * batch
+        tflops = flop / (mean_ms * 1e-3) / 1e12
+        r = {
+            "shape": f"{rows}x{cols}", "rhs": batch, "us_mean": round(mean_ms * 1e3, 2),
+            "roofline": {
+                "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                "note": "algorithmic FLOP (2*rows*cols*rhs); the kernel issues twice that on the "
+                        "matrix cores (x split into hi/lo f16 parts)",
+            },
+        }
+        log(f"bench:   {r['us_mean']} us, {r['roofline']['achieved']} TFLOP/s algorithmic = "
+            f"{100 * r['roofline']['frac']:.1f}% of the f16 MFMA peak")
+        out.append(r)
+        del bufsets, ys, xb
+    del mats
+    return out
+
+
 def hip_kernel(plan) -> str:
     """The HIP kernel family the planner picked (plan[0] == -2: matrix cores)."""
     return "affine_mfma_kernel" if plan[0] == -2 else "affine_gemv_kernel"
@@ -175,6 +215,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-metric", action="store_true",
                     help="time only the 5120x17408 shapes (for profiling runs)")
+    ap.add_argument("--only-wide", action="store_true",
+                    help="time only the config-4 wide block (for profiling runs)")
+    ap.add_argument("--wide-steps", type=int, default=30)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run plain copies of MIB MiB (counter calibration for profiling)")
     args = ap.parse_args()
@@ -189,8 +232,8 @@ def main() -> int:
     log(f"bench: device {gpu.name()}, steps={args.steps} warmup={args.warmup} copies={args.copies}")
     if args.copy_calibration:
         copy_calibration(gpu, args.copy_calibration, 8)
-    shapes = [("down", synth.MLP_SHAPES["down"])]
-    if not args.only_metric:
+    shapes = [] if args.only_wide else [("down", synth.MLP_SHAPES["down"])]
+    if not args.only_metric and not args.only_wide:
         shapes.append(("gate_up", synth.MLP_SHAPES["gate_up"]))
     results = []
     metric_matrix = None
@@ -230,6 +273,11 @@ def main() -> int:
             del bufsets, ys, xb
         del mats
 
+    wide = [] if args.only_metric else bench_wide(gpu, args)
+    if args.only_wide:
+        print(json.dumps({"wide": wide}), flush=True)
+        gpu.close()
+        return 0
     head = next(r for r in results if r["tag"] == "down" and r["batch"] == 1)
     b3 = next(r for r in results if r["tag"] == "down" and r["batch"] == 3)
     cpu = None
@@ -269,6 +317,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "results": results,
+        "wide": wide,
     }
     print(json.dumps(line), flush=True)
     gpu.close()
