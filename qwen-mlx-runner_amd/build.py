@@ -31,7 +31,9 @@ SOURCES = [
     ("affine_mfma.hip", ["-x", "hip"]),
     ("affine_rows.hip", ["-x", "hip"]),
     ("misc_kernels.hip", ["-x", "hip"]),
-    ("wide_mfma.hip", ["-x", "hip"]),
+    # MFMA accumulators in VGPRs: the wide kernel's FP32 epilogue adds into
+    # the same registers its bias MFMAs accumulate into.
+    ("wide_mfma.hip", ["-x", "hip", "-mllvm", "-amdgpu-mfma-vgpr-form"]),
 ]
 
 
@@ -45,7 +47,7 @@ def hipcc() -> str:
 def _compile(src: str, lang: list[str]) -> Path:
     obj = BUILD / (src + ".o")
     cmd = [hipcc(), *COMMON, *lang, "-c", str(CSRC / src), "-o", str(obj)]
-    if lang[-1] == "hip":
+    if lang[:2] == ["-x", "hip"]:
         cmd[1:1] = DEVICE_FLAGS
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
