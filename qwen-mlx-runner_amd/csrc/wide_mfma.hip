@@ -48,6 +48,7 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPrepThreads = 256;
 constexpr int kKRanges = 4;                      // K ranges per workgroup
+constexpr int kFirstHalf17 = 10;                  // row tiles of the first half at NRT = 17
 constexpr int kWaves = 2 * kKRanges;              // two row halves per K range
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRhsBlock = 32;                     // RHS per workgroup and per image
@@ -72,9 +73,15 @@ template <int META>
 constexpr size_t wave_meta_bytes(int nrt) {
     return size_t(16) * nrt * MetaCfg<META>::CG * (4 + MetaCfg<META>::BSZ);
 }
+// Row tiles of the first row half (waves 0-3). The hardware issues the
+// older of two waves sharing a SIMD first, so the first half gets the larger
+// share of the row tiles and both halves finish at about the same time.
+constexpr int first_half_tiles(int nrt) { return nrt == 17 ? kFirstHalf17 : (nrt + 1) / 2; }
 template <int META>
 constexpr size_t wide_lds_bytes(int nrt) {
-    const size_t meta = kWaves * (wave_meta_bytes<META>((nrt + 1) / 2) + MetaCfg<META>::CG * 4);
+    const size_t meta = kKRanges * (wave_meta_bytes<META>(first_half_tiles(nrt)) +
+                                    wave_meta_bytes<META>(nrt - first_half_tiles(nrt))) +
+                        kWaves * MetaCfg<META>::CG * 4;
     const size_t red = size_t(kKRanges) * nrt * 2 * 4 * 64 * 4;  // [K range][rt][ct][v][lane] f32
     return meta > red ? meta : red;
 }
@@ -164,8 +171,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
     using MC = MetaCfg<META>;
     constexpr int CG = MC::CG;
     constexpr int CQ = CG / 4;  // quads per chunk
-    constexpr int NRT0 = (NRT + 1) / 2;
-    constexpr int MRW = int(wave_meta_bytes<META>(NRT0));
+    constexpr int NRT0 = first_half_tiles(NRT);
+    constexpr int MR0 = int(wave_meta_bytes<META>(NRT0)), MR1 = int(wave_meta_bytes<META>(NRT - NRT0));
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: K range, rows, LDS regions
@@ -228,62 +235,67 @@ __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
                 sop[ct] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ir, int(so + ct * 64), base, 0));
         };
 
-        // Metadata chunk staging (this wave's region; only this wave reads it).
-        unsigned char *wm = lds + size_t(wave) * MRW;
-        float *ms = reinterpret_cast<float *>(wm);                       // s' [NTW*16][CG]
-        unsigned char *mbias = wm + size_t(NRT0) * 16 * CG * 4;          // b  [NTW*16][CG]
-        float *mfac = reinterpret_cast<float *>(lds + size_t(kWaves) * MRW) + wave * CG;
-        auto stage_meta = [&](uint32_t gc0, uint32_t ngc, auto nb_c) {
-            constexpr int NB = decltype(nb_c)::value;  // items per lane in flight at once
-            // Factors of the chunk's groups.
-            if (lane < CG) {
-                const uint32_t g = gc0 + uint32_t(lane);
-                const uint32_t off = uint32_t(lane) < ngc ? (g * p.ntb + tb) * kImgBytes + kImgFac : kOut;
-                mfac[lane] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ir, int(off), 0, 0));
-            }
-            wave_lds_sync();
-            // Items (row, quad): 4 groups of s and b of one row.
-            constexpr int ITEMS = NTW * 16 * CQ;
-            constexpr int PER_LANE = (ITEMS + 63) / 64;
+        // Metadata chunk staging (this wave's region; only this wave reads
+        // it): every load of a chunk is issued first (meta_issue), the
+        // conversion and LDS writes follow (meta_commit).
+        unsigned char *wm = lds + (rh ? size_t(kKRanges) * MR0 + size_t(kr) * MR1 : size_t(kr) * MR0);
+        float *ms = reinterpret_cast<float *>(wm);                  // s' [NTW*16][CG]
+        unsigned char *mbias = wm + size_t(NTW) * 16 * CG * 4;      // b  [NTW*16][CG]
+        float *mfac = reinterpret_cast<float *>(lds + size_t(kKRanges) * (MR0 + MR1)) + wave * CG;
+        constexpr int ITEMS = NTW * 16 * CQ;  // (row, quad): 4 groups of s and b of one row
+        constexpr int PER_LANE = (ITEMS + 63) / 64;
+        using Raw = std::conditional_t<META == 0, u4, u2>;
+        struct Staged {
+            Raw s[PER_LANE], b[PER_LANE];
+            float fac;  // factor of group gc0 + lane (lanes < CG)
+        };
+        auto meta_issue = [&](Staged &st, uint32_t gc0, uint32_t ngc) {
+            const uint32_t foff = uint32_t(lane) < ngc ? ((gc0 + uint32_t(lane)) * p.ntb + tb) * kImgBytes + kImgFac : kOut;
+            st.fac = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ir, int(foff), 0, 0));
             const uint32_t nqc = ngc / 4;
-            for (int i0 = 0; i0 < PER_LANE; i0 += NB)
 #pragma unroll
-                for (int i1 = 0; i1 < NB; ++i1) {
-                    const int i = i0 + i1;
-                    const uint32_t it = uint32_t(lane) + uint32_t(i) * 64;
-                    const uint32_t rl = it / CQ, j = it - rl * CQ;
-                    const bool live = it < uint32_t(ITEMS) && j < nqc && wrow0 + rl < p.rows;
-                    const uint32_t moff = live ? (wrow0 + rl) * m_pitch + (gc0 + 4 * j) * (META == 0 ? 4 : 2) : kOut;
-                    float sv[4], bv[4];
-                    u2 braw{0u, 0u};
+            for (int i = 0; i < PER_LANE; ++i) {
+                const uint32_t it = uint32_t(lane) + uint32_t(i) * 64;
+                const uint32_t rl = it / CQ, j = it - rl * CQ;
+                const bool live = it < uint32_t(ITEMS) && j < nqc && wrow0 + rl < p.rows;
+                const uint32_t moff = live ? (wrow0 + rl) * m_pitch + (gc0 + 4 * j) * (META == 0 ? 4 : 2) : kOut;
+                if constexpr (META == 0) {
+                    st.s[i] = __builtin_amdgcn_raw_buffer_load_b128(sr, int(moff), 0, 0);
+                    st.b[i] = __builtin_amdgcn_raw_buffer_load_b128(br, int(moff), 0, 0);
+                } else {
+                    st.s[i] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(sr, int(moff), 0, 0));
+                    st.b[i] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(br, int(moff), 0, 0));
+                }
+            }
+        };
+        auto meta_commit = [&](const Staged &st) {
+            if (lane < CG) mfac[lane] = st.fac;
+            wave_lds_sync();
+#pragma unroll
+            for (int i = 0; i < PER_LANE; ++i) {
+                const uint32_t it = uint32_t(lane) + uint32_t(i) * 64;
+                const uint32_t rl = it / CQ, j = it - rl * CQ;
+                if (it < uint32_t(ITEMS)) {
+                    float sv[4];
                     if constexpr (META == 0) {
-                        const u4 s4 = __builtin_amdgcn_raw_buffer_load_b128(sr, int(moff), 0, 0);
-                        const u4 b4 = __builtin_amdgcn_raw_buffer_load_b128(br, int(moff), 0, 0);
 #pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            sv[k] = __uint_as_float(s4[k]);
-                            bv[k] = __uint_as_float(b4[k]);
-                        }
+                        for (int k = 0; k < 4; ++k) sv[k] = __uint_as_float(st.s[i][k]);
                     } else {
-                        const u2 s2 = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(sr, int(moff), 0, 0));
-                        braw = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(br, int(moff), 0, 0));
 #pragma unroll
                         for (int k = 0; k < 2; ++k) {
-                            sv[2 * k] = __uint_as_float(s2[k] << 16);
-                            sv[2 * k + 1] = __uint_as_float(s2[k] & 0xFFFF0000u);
+                            sv[2 * k] = __uint_as_float(st.s[i][k] << 16);
+                            sv[2 * k + 1] = __uint_as_float(st.s[i][k] & 0xFFFF0000u);
                         }
-                        (void)bv;
                     }
-                    if (i < PER_LANE && it < uint32_t(ITEMS)) {
-                        const float4 fac = *reinterpret_cast<const float4 *>(mfac + 4 * j);
-                        *reinterpret_cast<float4 *>(ms + rl * CG + 4 * j) =
-                            float4{sv[0] * fac.x, sv[1] * fac.y, sv[2] * fac.z, sv[3] * fac.w};
-                        if constexpr (META == 0)
-                            *reinterpret_cast<float4 *>(mbias + (rl * CG + 4 * j) * 4) = float4{bv[0], bv[1], bv[2], bv[3]};
-                        else
-                            *reinterpret_cast<u2 *>(mbias + (rl * CG + 4 * j) * 2) = braw;
-                    }
+                    const float4 fac = *reinterpret_cast<const float4 *>(mfac + 4 * j);
+                    *reinterpret_cast<float4 *>(ms + rl * CG + 4 * j) =
+                        float4{sv[0] * fac.x, sv[1] * fac.y, sv[2] * fac.z, sv[3] * fac.w};
+                    if constexpr (META == 0)
+                        *reinterpret_cast<u4 *>(mbias + (rl * CG + 4 * j) * 4) = st.b[i];
+                    else
+                        *reinterpret_cast<u2 *>(mbias + (rl * CG + 4 * j) * 2) = st.b[i];
                 }
+            }
             wave_lds_sync();
         };
 
@@ -356,22 +368,30 @@ __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
         };
 
         if (ga < gb) {
-            // First requests (codes and x of the first group, the first
-            // quad's S), then the first chunk's metadata with every item in
-            // flight (nothing else is live yet); later chunks stage 4 items
-            // at a time.
+            // All first requests in flight together: the first chunk's
+            // metadata, then the first group's codes and x and the first
+            // quad's S; the metadata commit then waits for its own loads only.
             h8 xa[8], xb[8];
             float sa[2], sb[2];
-            load_x(xa, ga);
-            load_s(sa, ga);
+            {
+                Staged st;
+                meta_issue(st, ga, min(uint32_t(CG), gb - ga));
+                load_x(xa, ga);
+                load_s(sa, ga);
 #pragma unroll
-            for (int rt = 0; rt < NTW; ++rt) load_codes(rt, ga);
-            stage_meta(ga, min(uint32_t(CG), gb - ga), std::integral_constant<int, (NTW * 16 * CQ + 63) / 64>{});
+                for (int rt = 0; rt < NTW; ++rt) load_codes(rt, ga);
+                __builtin_amdgcn_sched_barrier(0);  // every request before any use
+                meta_commit(st);
+            }
 #pragma unroll
             for (int rt = 0; rt < NTW; ++rt) acc[rt][0] = acc[rt][1] = zero;
             for (uint32_t gc0 = ga; gc0 < gb; gc0 += CG) {
                 const uint32_t ngc = min(uint32_t(CG), gb - gc0);
-                if (gc0 != ga) stage_meta(gc0, ngc, std::integral_constant<int, 4>{});
+                if (gc0 != ga) {
+                    Staged st;
+                    meta_issue(st, gc0, ngc);
+                    meta_commit(st);
+                }
                 for (uint32_t gl = 0; gl < ngc; gl += 4) {
                     const uint32_t g = gc0 + gl;
                     load_s(sb, min(g + 4, gb - 4));  // next quad (last: a harmless reload)
