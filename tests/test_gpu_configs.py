@@ -95,10 +95,14 @@ def test_config4_wide_block(gpu, batch):
 
 @pytest.mark.parametrize("rows,cols,batch,meta", [(300, 1024, 100, "bf16"), (128, 512, 64, "f32"),
                                                   (17, 512, 5, "bf16"), (1000, 2048, 256, "f32"),
-                                                  (250, 1536, 65, "bf16")])
+                                                  (250, 1536, 65, "bf16"), (290, 4096, 40, "f32"),
+                                                  (600, 6400, 33, "bf16"), (17000, 512, 128, "bf16")])
 def test_wide_block_tails_and_metadata(gpu, rows, cols, batch, meta):
-    """Wide blocks at ragged row and column counts (row blocks of 128,
-    column blocks of 64), both wide names, against the FP64 oracle."""
+    """Wide blocks at ragged row and RHS counts, both wide names, against
+    the FP64 oracle. The kernel's K quarters hold 16 groups at cols 4096 and
+    25 at cols 6400, past one metadata chunk (12 groups for F32 metadata, 20
+    for BF16), so those cases stage several chunks per wave; 17000 rows take
+    the 272-row workgroups and a partial last row block."""
     rng = np.random.default_rng(rows + batch)
     w = rng.integers(0, 2**32, rows * cols // 8, dtype=np.uint32)
     sf = rng.uniform(0.002, 0.02, rows * cols // 64).astype(np.float32)
