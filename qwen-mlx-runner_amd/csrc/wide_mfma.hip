@@ -14,18 +14,20 @@
 //      RHS): the group's eight MFMA A fragments (2 K steps x 2 RHS tiles x
 //      hi/lo, 1 KB each, in lane order), the group sums S of the 32 RHS and
 //      the factor 2^(20+e) of the block's power-of-two scale 2^-e.
-//   2. wide_mfma_kernel: a workgroup of eight waves owns 16*NRT rows x 32
-//      RHS. K is split into four ranges of whole quads of groups and the row
-//      tiles into two halves; wave w takes K range w%4 and half w/4, so the
-//      two waves sharing a SIMD have the same instruction mix and one's
-//      matrix-core work overlaps the other's vector-ALU work. A wave covers
-//      both RHS tiles of its row tiles (8 FP32 accumulators per lane and row
-//      tile). Per group it loads the 8 x fragments (one group ahead) and one
-//      8-byte code piece per row tile (the next group's piece is requested as
-//      soon as this one is unpacked) straight into registers. Scales (already
-//      multiplied by the image factors) and biases of the wave's rows and K
-//      range go through LDS, staged by the wave itself. At the end the four
-//      K ranges meet in LDS and are added in K order.
+//   2. wide_mfma_kernel: a workgroup of four waves (one per SIMD) owns
+//      16*NRT rows x 32 RHS. Wave w takes every fourth quant group, g = w
+//      (mod 4), so the four waves read the four 32-byte pieces of the same
+//      128-byte code lines at about the same time (one L2 fetch, three L1
+//      hits) and each x fragment is loaded once. A wave covers all row tiles
+//      and both RHS tiles (8 FP32 accumulators per lane and row tile; a
+//      second wave per SIMD gains nothing here, the vector ALU and the
+//      matrix cores of a SIMD barely overlap). Per group it loads the 8 x
+//      fragments (one group ahead) and one 8-byte code piece per row tile
+//      (the next group's piece is requested as soon as this one is unpacked)
+//      straight into registers. Scales (already multiplied by the image
+//      factors) and biases stream through LDS in chunks of 16 groups, two
+//      buffers, loaded by the whole workgroup one chunk ahead. At the end the
+//      four group classes meet in LDS and are added in a fixed order.
 // With NRT = 17 the 17408-row MLP matrix is 64 row blocks, which with four
 // 32-RHS blocks at 128 RHS is one workgroup per CU of the 256.
 #include <hip/hip_runtime.h>
@@ -47,9 +49,8 @@ using namespace mfma;
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPrepThreads = 256;
-constexpr int kKRanges = 4;                      // K ranges per workgroup
-constexpr int kFirstHalf17 = 10;                  // row tiles of the first half at NRT = 17
-constexpr int kWaves = 2 * kKRanges;              // two row halves per K range
+constexpr int kKRanges = 4;                      // group classes (g mod 4) per workgroup
+constexpr int kWaves = kKRanges;                  // one wave per group class
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRhsBlock = 32;                     // RHS per workgroup and per image
 constexpr int kFragBytes = 1024;                  // one MFMA A fragment (64 lanes x 16 B)
@@ -58,31 +59,19 @@ constexpr int kImgFac = kImgS + kRhsBlock * 4;    // factor f32
 constexpr int kImgBytes = 8448;                   // image stride (16-byte multiple)
 static_assert(kImgFac + 4 <= kImgBytes, "image layout");
 
-// Metadata staged per wave and chunk of groups: s' (f32) and b (f32 for F32
-// metadata, bf16 for BF16), [row][group] with a pitch of CG entries; CG is a
-// multiple of 4 that is 4 mod 8, so the 16 rows one read touches fall in 16
-// different banks.
+// Metadata chunk in LDS (one of two buffers): s' (f32) and b (f32 for F32
+// metadata, bf16 for BF16) of 16 groups, [row][group] with a pitch of 20
+// entries (4 mod 8: the 16 rows one read touches fall in 16 banks).
+constexpr int kCG = 16;  // groups per chunk: one quad per group class
+constexpr int kPitch = 20;
 template <int META>
-struct MetaCfg {
-    static constexpr int CG = META == 0 ? 12 : 20;  // groups per chunk
-    static constexpr int BSZ = META == 0 ? 4 : 2;   // bytes of a staged bias
-    static_assert(CG % 8 == 4, "pitch");
-};
-
-template <int META>
-constexpr size_t wave_meta_bytes(int nrt) {
-    return size_t(16) * nrt * MetaCfg<META>::CG * (4 + MetaCfg<META>::BSZ);
+constexpr size_t meta_buf_bytes(int nrt) {
+    return size_t(16) * nrt * kPitch * (4 + (META == 0 ? 4 : 2));
 }
-// Row tiles of the first row half (waves 0-3). The hardware issues the
-// older of two waves sharing a SIMD first, so the first half gets the larger
-// share of the row tiles and both halves finish at about the same time.
-constexpr int first_half_tiles(int nrt) { return nrt == 17 ? kFirstHalf17 : (nrt + 1) / 2; }
 template <int META>
 constexpr size_t wide_lds_bytes(int nrt) {
-    const size_t meta = kKRanges * (wave_meta_bytes<META>(first_half_tiles(nrt)) +
-                                    wave_meta_bytes<META>(nrt - first_half_tiles(nrt))) +
-                        kWaves * MetaCfg<META>::CG * 4;
-    const size_t red = size_t(kKRanges) * nrt * 2 * 4 * 64 * 4;  // [K range][rt][ct][v][lane] f32
+    const size_t meta = 2 * meta_buf_bytes<META>(nrt);
+    const size_t red = size_t(kKRanges) * nrt * 2 * 4 * 64 * 4;  // [class][rt][ct][v][lane] f32
     return meta > red ? meta : red;
 }
 
@@ -161,22 +150,16 @@ __device__ __forceinline__ h8 unpack_word(uint32_t wd) {
 }
 
 // ---- 2. The contraction. grid: row blocks (padded to a multiple of 8) x
-// NTB, 512 threads. Wave w takes K range w%4 and row half w/4 (the first
-// ceil(NRT/2) row tiles or the rest); the two waves of a K range share a
-// SIMD, so one's matrix-core work overlaps the other's vector-ALU work.
-// Lane (r16, q): row r16 of every row tile, K chunk q of every K step; D
-// element v of a tile is RHS 4q + v of its 16-RHS tile. ----
+// NTB, 256 threads. Lane (r16, q): row r16 of every row tile, K chunk q of
+// every K step; D element v of a tile is RHS 4q + v of its 16-RHS tile. ----
 template <int META, int NRT>
 __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
-    using MC = MetaCfg<META>;
-    constexpr int CG = MC::CG;
-    constexpr int CQ = CG / 4;  // quads per chunk
-    constexpr int NRT0 = first_half_tiles(NRT);
-    constexpr int MR0 = int(wave_meta_bytes<META>(NRT0)), MR1 = int(wave_meta_bytes<META>(NRT - NRT0));
+    constexpr int ROWS = 16 * NRT;
+    constexpr int BSZ = META == 0 ? 4 : 2;
+    constexpr size_t BUF = meta_buf_bytes<META>(NRT);
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: K range, rows, LDS regions
-    const int kr = wave & 3, rh = wave >> 2;
+    const int kr = __builtin_amdgcn_readfirstlane(tid >> 6);  // the wave's group class (uniform)
     const int lane = tid & 63;
     const int r16 = lane & 15, q = lane >> 4;
     // XCD-aware order: workgroup i runs on XCD i % 8, so the NTB workgroups
@@ -186,39 +169,99 @@ __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
     const uint32_t tb = slot % p.ntb;
     const uint32_t rb = (slot / p.ntb) * 8 + xcd;
     if (rb >= p.nrb) return;
-    const uint32_t row0 = rb * 16 * NRT;
+    const uint32_t row0 = rb * ROWS;
     const uint32_t G = p.cols / 64;
-    const uint32_t nq = G / 4;
-    const uint32_t qa = uint32_t(kr) * nq / kKRanges, qb = uint32_t(kr + 1) * nq / kKRanges;
-    const uint32_t ga = qa * 4, gb = qb * 4;  // this wave's groups [ga, gb)
+    const uint32_t nch = (G + kCG - 1) / kCG;
     const uint32_t row_bytes = p.cols / 2;
-    const int rtb = rh ? NRT0 : 0;  // first row tile of this wave
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t *>(p.w), 0, int(p.w_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t ir = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<unsigned char *>(p.img), 0, int(p.img_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.s), 0, int(p.m_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.b), 0, int(p.m_bytes), kRsrcWord3);
-    const uint32_t m_pitch = G * (META == 0 ? 4 : 2);
+    const uint32_t m_pitch = G * BSZ;
     const f4 zero{0.f, 0.f, 0.f, 0.f};
-    float *red = reinterpret_cast<float *>(lds);  // final reduction [kr][row tile][ct][v][lane]
+    float *red = reinterpret_cast<float *>(lds);  // final reduction [class][row tile][ct][v][lane]
 
-    // The wave's share: NTW row tiles from rtb, K range [ga, gb).
-    auto run = [&](auto ntw_c) {
-        constexpr int NTW = decltype(ntw_c)::value;
-        const uint32_t wrow0 = row0 + uint32_t(rtb) * 16;
+    // Metadata chunk c (groups 16c..16c+15) of all the workgroup's rows,
+    // staged by every thread: item (row, j) = groups 16c+4j..16c+4j+3 of one
+    // row; thread tid always has j = tid % 4, so it needs the image factors
+    // of 4 groups only. Past the matrix (rows or groups) everything is zero.
+    constexpr int ITEMS = ROWS * 4;
+    constexpr int PER_T = (ITEMS + kThreads - 1) / kThreads;
+    using Raw = std::conditional_t<META == 0, u4, u2>;
+    struct MStage {
+        Raw s[PER_T], b[PER_T];
+        float fac[4];
+    };
+    const uint32_t mj = uint32_t(tid) & 3;
+    auto meta_issue = [&](MStage &st, uint32_t c) {
+        const uint32_t g4 = c * kCG + 4 * mj;  // first group of this thread's items
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t g = g4 + uint32_t(k);
+            const uint32_t off = g < G ? (g * p.ntb + tb) * kImgBytes + kImgFac : kOut;
+            st.fac[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ir, int(off), 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const uint32_t it = uint32_t(tid) + uint32_t(i) * kThreads;
+            const uint32_t rl = it >> 2;
+            const bool live = it < uint32_t(ITEMS) && row0 + rl < p.rows && g4 < G;
+            const uint32_t moff = live ? (row0 + rl) * m_pitch + g4 * BSZ : kOut;
+            if constexpr (META == 0) {
+                st.s[i] = __builtin_amdgcn_raw_buffer_load_b128(sr, int(moff), 0, 0);
+                st.b[i] = __builtin_amdgcn_raw_buffer_load_b128(br, int(moff), 0, 0);
+            } else {
+                st.s[i] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(sr, int(moff), 0, 0));
+                st.b[i] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(br, int(moff), 0, 0));
+            }
+        }
+    };
+    auto meta_commit = [&](const MStage &st, uint32_t c) {
+        unsigned char *buf = lds + (c & 1) * BUF;
+        float *ms = reinterpret_cast<float *>(buf);
+        unsigned char *mb = buf + size_t(ROWS) * kPitch * 4;
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const uint32_t it = uint32_t(tid) + uint32_t(i) * kThreads;
+            const uint32_t rl = it >> 2;
+            if (it < uint32_t(ITEMS)) {
+                float sv[4];
+                if constexpr (META == 0) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) sv[k] = __uint_as_float(st.s[i][k]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        sv[2 * k] = __uint_as_float(st.s[i][k] << 16);
+                        sv[2 * k + 1] = __uint_as_float(st.s[i][k] & 0xFFFF0000u);
+                    }
+                }
+                *reinterpret_cast<float4 *>(ms + rl * kPitch + 4 * mj) =
+                    float4{sv[0] * st.fac[0], sv[1] * st.fac[1], sv[2] * st.fac[2], sv[3] * st.fac[3]};
+                *reinterpret_cast<Raw *>(mb + (rl * kPitch + 4 * mj) * BSZ) = st.b[i];
+            }
+        }
+    };
+
+    // The wave's share: all row tiles, groups kr, kr+4, ...
+    {
+        constexpr int NTW = NRT;
         // Code piece of row tile rt: words 2q, 2q+1 of the group for row
-        // wrow0 + 16 rt + r16. The row tile and group move only the scalar
-        // offset; the buffer range check covers vector plus scalar offset,
-        // so rows past the matrix read zeros.
-        const uint32_t cbase = (wrow0 + uint32_t(r16)) * row_bytes + uint32_t(q) * 8;
+        // row0 + 16 rt + r16. The row tile and group move only the
+        // scalar offset; the buffer range check covers vector plus scalar
+        // offset, so rows past the matrix read zeros (and groups past the
+        // row read the next row's codes, which meet zero scales).
+        const uint32_t cbase = (row0 + uint32_t(r16)) * row_bytes + uint32_t(q) * 8;
         const uint32_t cstride = 16 * row_bytes;
         u2 cw[NTW];
         auto load_codes = [&](int rt, uint32_t g) {
             cw[rt] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(
                                                  wr, int(cbase), int(uint32_t(rt) * cstride + g * 32), 0));
         };
-        // x fragments of group g: f = (ks*2 + ct)*2 + hl, lane i at 16 i.
+        // x fragments of group g: f = (ks*2 + ct)*2 + hl, lane i at 16 i
+        // (past the last group: past the images, zeros).
         const uint32_t xo = uint32_t(lane) * 16;
         auto load_x = [&](h8 (&xf)[8], uint32_t g) {
             const int base = int((g * p.ntb + tb) * kImgBytes);
@@ -226,95 +269,31 @@ __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
             for (int f = 0; f < 8; ++f)
                 xf[f] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(ir, int(xo), base + f * kFragBytes, 0));
         };
-        // Bias A operands of the quad at group g0: S[g0 + q][16 ct + r16].
-        const uint32_t so = uint32_t(q) * p.ntb * kImgBytes + kImgS + uint32_t(r16) * 4;
-        auto load_s = [&](float (&sop)[2], uint32_t g0) {
-            const int base = int((g0 * p.ntb + tb) * kImgBytes);
+        // Bias A operands of chunk c: S[16c + 4q + kr][16 ct + r16].
+        const uint32_t so = uint32_t(q) * 4 * p.ntb * kImgBytes + kImgS + uint32_t(r16) * 4;
+        auto load_s = [&](float (&sop)[2], uint32_t c) {
+            const int base = int(((c * kCG + uint32_t(kr)) * p.ntb + tb) * kImgBytes);
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct)
                 sop[ct] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ir, int(so + ct * 64), base, 0));
         };
 
-        // Metadata chunk staging (this wave's region; only this wave reads
-        // it): every load of a chunk is issued first (meta_issue), the
-        // conversion and LDS writes follow (meta_commit).
-        unsigned char *wm = lds + (rh ? size_t(kKRanges) * MR0 + size_t(kr) * MR1 : size_t(kr) * MR0);
-        float *ms = reinterpret_cast<float *>(wm);                  // s' [NTW*16][CG]
-        unsigned char *mbias = wm + size_t(NTW) * 16 * CG * 4;      // b  [NTW*16][CG]
-        float *mfac = reinterpret_cast<float *>(lds + size_t(kKRanges) * (MR0 + MR1)) + wave * CG;
-        constexpr int ITEMS = NTW * 16 * CQ;  // (row, quad): 4 groups of s and b of one row
-        constexpr int PER_LANE = (ITEMS + 63) / 64;
-        using Raw = std::conditional_t<META == 0, u4, u2>;
-        struct Staged {
-            Raw s[PER_LANE], b[PER_LANE];
-            float fac;  // factor of group gc0 + lane (lanes < CG)
-        };
-        auto meta_issue = [&](Staged &st, uint32_t gc0, uint32_t ngc) {
-            const uint32_t foff = uint32_t(lane) < ngc ? ((gc0 + uint32_t(lane)) * p.ntb + tb) * kImgBytes + kImgFac : kOut;
-            st.fac = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ir, int(foff), 0, 0));
-            const uint32_t nqc = ngc / 4;
-#pragma unroll
-            for (int i = 0; i < PER_LANE; ++i) {
-                const uint32_t it = uint32_t(lane) + uint32_t(i) * 64;
-                const uint32_t rl = it / CQ, j = it - rl * CQ;
-                const bool live = it < uint32_t(ITEMS) && j < nqc && wrow0 + rl < p.rows;
-                const uint32_t moff = live ? (wrow0 + rl) * m_pitch + (gc0 + 4 * j) * (META == 0 ? 4 : 2) : kOut;
-                if constexpr (META == 0) {
-                    st.s[i] = __builtin_amdgcn_raw_buffer_load_b128(sr, int(moff), 0, 0);
-                    st.b[i] = __builtin_amdgcn_raw_buffer_load_b128(br, int(moff), 0, 0);
-                } else {
-                    st.s[i] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(sr, int(moff), 0, 0));
-                    st.b[i] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(br, int(moff), 0, 0));
-                }
-            }
-        };
-        auto meta_commit = [&](const Staged &st) {
-            if (lane < CG) mfac[lane] = st.fac;
-            wave_lds_sync();
-#pragma unroll
-            for (int i = 0; i < PER_LANE; ++i) {
-                const uint32_t it = uint32_t(lane) + uint32_t(i) * 64;
-                const uint32_t rl = it / CQ, j = it - rl * CQ;
-                if (it < uint32_t(ITEMS)) {
-                    float sv[4];
-                    if constexpr (META == 0) {
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) sv[k] = __uint_as_float(st.s[i][k]);
-                    } else {
-#pragma unroll
-                        for (int k = 0; k < 2; ++k) {
-                            sv[2 * k] = __uint_as_float(st.s[i][k] << 16);
-                            sv[2 * k + 1] = __uint_as_float(st.s[i][k] & 0xFFFF0000u);
-                        }
-                    }
-                    const float4 fac = *reinterpret_cast<const float4 *>(mfac + 4 * j);
-                    *reinterpret_cast<float4 *>(ms + rl * CG + 4 * j) =
-                        float4{sv[0] * fac.x, sv[1] * fac.y, sv[2] * fac.z, sv[3] * fac.w};
-                    if constexpr (META == 0)
-                        *reinterpret_cast<u4 *>(mbias + (rl * CG + 4 * j) * 4) = st.b[i];
-                    else
-                        *reinterpret_cast<u2 *>(mbias + (rl * CG + 4 * j) * 2) = st.b[i];
-                }
-            }
-            wave_lds_sync();
-        };
-
         f4 acc[NTW][2];
-        // One group: codes of g in cw (their g+1 successors requested as
-        // each piece is unpacked), x fragments of g in xf. Software-pipelined
-        // by row tile: step rt issues the 8 MFMAs of tile rt and, on the
-        // vector ALU, the epilogue of tile rt-1 and the unpacking of tile
-        // rt+1; a scheduling barrier keeps the steps apart, which bounds the
-        // live registers.
-        auto group = [&](const h8 (&xf)[8], uint32_t g, uint32_t gl) {
-            const uint32_t gn = min(g + 1, gb - 1);  // last group: a harmless reload
-            h8 bc[2][2];                               // [tile parity][K step]
+        // One group (chunk buffer cb, class step i): codes of g in cw (their
+        // successors, group g+4, requested as each piece is unpacked), x
+        // fragments of g in xf. Software-pipelined by row tile: step rt
+        // issues the 8 MFMAs of tile rt and, on the vector ALU, the epilogue
+        // of tile rt-1 and the unpacking of tile rt+1; a scheduling barrier
+        // keeps the steps apart, which bounds the live registers.
+        auto group = [&](const h8 (&xf)[8], uint32_t g, const float *ms, int i) {
+            const float *msw = ms + r16 * kPitch + 4 * i + kr;
+            h8 bc[2][2];  // [tile parity][K step]
             f4 dp0 = zero, dp1 = zero;
             float svp = 0.f;
             bc[0][0] = unpack_word(cw[0].x);
             bc[0][1] = unpack_word(cw[0].y);
-            load_codes(0, gn);
-            float svn = ms[r16 * CG + gl];
+            load_codes(0, g + 4);
+            float svn = msw[0];
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int rt = 0; rt < NTW; ++rt) {
@@ -337,10 +316,10 @@ __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
                 if (rt + 1 < NTW) {
                     bc[(rt + 1) & 1][0] = unpack_word(cw[rt + 1].x);
                     bc[(rt + 1) & 1][1] = unpack_word(cw[rt + 1].y);
-                    load_codes(rt + 1, gn);
+                    load_codes(rt + 1, g + 4);
                 }
                 svp = svn;
-                if (rt + 1 < NTW) svn = ms[((rt + 1) * 16 + r16) * CG + gl];
+                if (rt + 1 < NTW) svn = msw[(rt + 1) * 16 * kPitch];
                 dp0 = d0;
                 dp1 = d1;
                 __builtin_amdgcn_sched_barrier(0);
@@ -351,89 +330,80 @@ __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
                 acc[NTW - 1][1][v] = __builtin_fmaf(svp, dp1[v], acc[NTW - 1][1][v]);
             }
         };
-        // Bias of the quad at chunk-local group gl0: acc += S x b over 4 groups.
-        auto bias = [&](const float (&sop)[2], uint32_t gl0) {
+        // Bias of the wave's four groups of a chunk: acc += S x b.
+        auto bias = [&](const float (&sop)[2], const unsigned char *mb) {
 #pragma unroll
             for (int rt = 0; rt < NTW; ++rt) {
-                const uint32_t e = (rt * 16 + r16) * CG + gl0 + q;
+                const uint32_t e = (rt * 16 + r16) * kPitch + 4 * q + kr;
                 float bvv;
                 if constexpr (META == 0)
-                    bvv = reinterpret_cast<const float *>(mbias)[e];
+                    bvv = reinterpret_cast<const float *>(mb)[e];
                 else
-                    bvv = __uint_as_float(uint32_t(reinterpret_cast<const uint16_t *>(mbias)[e]) << 16);
+                    bvv = __uint_as_float(uint32_t(reinterpret_cast<const uint16_t *>(mb)[e]) << 16);
 #pragma unroll
                 for (int ct = 0; ct < 2; ++ct)
                     acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(sop[ct], bvv, acc[rt][ct], 0, 0, 0);
             }
         };
 
-        if (ga < gb) {
-            // All first requests in flight together: the first chunk's
-            // metadata, then the first group's codes and x and the first
-            // quad's S; the metadata commit then waits for its own loads only.
-            h8 xa[8], xb[8];
-            float sa[2], sb[2];
-            {
-                Staged st;
-                meta_issue(st, ga, min(uint32_t(CG), gb - ga));
-                load_x(xa, ga);
-                load_s(sa, ga);
+        // All first requests in flight together (chunk 0's metadata, the
+        // first group's codes and x, chunk 0's S), then chunk 0 into LDS.
+        h8 xa[8], xb[8];
+        float sa[2], sb[2];
+        {
+            MStage st;
+            meta_issue(st, 0);
+            load_x(xa, uint32_t(kr));
+            load_s(sa, 0);
 #pragma unroll
-                for (int rt = 0; rt < NTW; ++rt) load_codes(rt, ga);
-                __builtin_amdgcn_sched_barrier(0);  // every request before any use
-                meta_commit(st);
-            }
+            for (int rt = 0; rt < NTW; ++rt) load_codes(rt, uint32_t(kr));
+            __builtin_amdgcn_sched_barrier(0);  // every request before any use
+            meta_commit(st, 0);
+        }
 #pragma unroll
-            for (int rt = 0; rt < NTW; ++rt) acc[rt][0] = acc[rt][1] = zero;
-            for (uint32_t gc0 = ga; gc0 < gb; gc0 += CG) {
-                const uint32_t ngc = min(uint32_t(CG), gb - gc0);
-                if (gc0 != ga) {
-                    Staged st;
-                    meta_issue(st, gc0, ngc);
-                    meta_commit(st);
-                }
-                for (uint32_t gl = 0; gl < ngc; gl += 4) {
-                    const uint32_t g = gc0 + gl;
-                    load_s(sb, min(g + 4, gb - 4));  // next quad (last: a harmless reload)
-                    load_x(xb, g + 1);
-                    group(xa, g, gl);
-                    load_x(xa, g + 2);
-                    group(xb, g + 1, gl + 1);
-                    load_x(xb, g + 3);
-                    group(xa, g + 2, gl + 2);
-                    load_x(xa, min(g + 4, gb - 1));  // last quad: a harmless reload
-                    group(xb, g + 3, gl + 3);
-                    bias(sa, gl);
-                    sa[0] = sb[0];
-                    sa[1] = sb[1];
-                }
-                wave_lds_sync();  // this chunk's metadata reads precede the next chunk's writes
-            }
-        } else {
-#pragma unroll
-            for (int rt = 0; rt < NTW; ++rt) acc[rt][0] = acc[rt][1] = zero;
+        for (int rt = 0; rt < NTW; ++rt) acc[rt][0] = acc[rt][1] = zero;
+        lds_barrier();
+        // Chunk c: this wave's groups 16c + kr + 4i, i = 0..3. The next
+        // chunk's metadata is requested first and committed to the other
+        // buffer at the end (after the last chunk: zeros, never read), so the
+        // loop body has no branch.
+        for (uint32_t c = 0; c < nch; ++c) {
+            const unsigned char *buf = lds + (c & 1) * BUF;
+            const float *ms = reinterpret_cast<const float *>(buf);
+            const unsigned char *mb = buf + size_t(ROWS) * kPitch * 4;
+            const uint32_t g = c * kCG + uint32_t(kr);
+            MStage st;
+            meta_issue(st, c + 1);
+            load_s(sb, c + 1);
+            load_x(xb, g + 4);
+            group(xa, g, ms, 0);
+            load_x(xa, g + 8);
+            group(xb, g + 4, ms, 1);
+            load_x(xb, g + 12);
+            group(xa, g + 8, ms, 2);
+            load_x(xa, g + 16);
+            group(xb, g + 12, ms, 3);
+            bias(sa, mb);
+            sa[0] = sb[0];
+            sa[1] = sb[1];
+            meta_commit(st, c + 1);
+            lds_barrier();
         }
 
-        // The K ranges meet in LDS once every wave is done with its
-        // metadata region.
-        lds_barrier();
+        // The group classes meet in LDS (the metadata buffers are free).
 #pragma unroll
         for (int rt = 0; rt < NTW; ++rt)
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    red[(((kr * NRT + rtb + rt) * 2 + ct) * 4 + v) * 64 + lane] = acc[rt][ct][v];
-    };
-    if (rh == 0)
-        run(std::integral_constant<int, NRT0>{});
-    else
-        run(std::integral_constant<int, NRT - NRT0>{});
+                    red[(((kr * NRT + rt) * 2 + ct) * 4 + v) * 64 + lane] = acc[rt][ct][v];
+    }
     lds_barrier();
-    // Wave w writes the (row tile, ct, v) combinations w, w+8, ...: lane
-    // (r16, q) holds row 16 rt + r16 and RHS 16 ct + 4 q + v; the four K
-    // ranges are added in order.
-    for (int cmb = wave; cmb < NRT * 8; cmb += kWaves) {
+    // Wave w writes the (row tile, ct, v) combinations w, w+4, ...: lane
+    // (r16, q) holds row 16 rt + r16 and RHS 16 ct + 4 q + v; the four group
+    // classes are added in order.
+    for (int cmb = kr; cmb < NRT * 8; cmb += kWaves) {
         float sum = 0.f;
 #pragma unroll
         for (int k = 0; k < kKRanges; ++k) sum += red[(k * NRT * 8 + cmb) * 64 + lane];
@@ -506,12 +476,15 @@ bool wide_mfma_supported(const AffineArgs &a) {
     if (a.bits != 4 || a.group != 64) return false;
     if (a.meta != Meta::F32 && a.meta != Meta::BF16) return false;
     if (a.batch < 1 || a.batch > 256) return false;
-    if (a.cols % 256 != 0) return false;  // whole quads of groups
+    if (a.cols % 256 != 0) return false;  // whole quads of groups (metadata items)
     const uintptr_t al = reinterpret_cast<uintptr_t>(a.w) | reinterpret_cast<uintptr_t>(a.s) |
                          reinterpret_cast<uintptr_t>(a.b);
-    // Code offsets reach one workgroup's rows past the matrix.
-    const uint64_t w_span = (uint64_t(a.rows) + 16 * 17) * a.cols / 2;
-    const uint64_t img = uint64_t(a.cols / 64) * ((a.batch + kRhsBlock - 1) / kRhsBlock) * kImgBytes;
+    // 32-bit buffer offsets: codes reach one workgroup's rows plus a row
+    // past the matrix, images and prefetches up to a chunk plus a quad of
+    // groups past the last one (all read as zeros).
+    const uint64_t w_span = (uint64_t(a.rows) + 16 * 17 + 2) * a.cols / 2;
+    const uint64_t ntb = (a.batch + kRhsBlock - 1) / kRhsBlock;
+    const uint64_t img = (uint64_t(a.cols / 64) + kCG + 8) * ntb * kImgBytes;
     return al % 16 == 0 && uint64_t(a.batch) * a.cols * 4 < (1ull << 31) && w_span < (1ull << 31) &&
            img < (1ull << 31);
 }
