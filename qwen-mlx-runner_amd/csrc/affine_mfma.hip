@@ -494,6 +494,7 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
     // Score = |log(waves/target)| plus twice the log of the split imbalance.
     const uint32_t cus = lim.num_cus > 0 ? uint32_t(lim.num_cus) : 256u;
     double best = 1e30;
+    uint32_t best_resident = 1;
     const uint32_t tpe = 8 / a.bits;  // K tiles per 128-byte load entry
     for (uint32_t ns = 1; ns <= tiles && ns <= kMaxSplits; ++ns) {
         uint32_t tps = (tiles + ns - 1) / ns;
@@ -514,6 +515,7 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
             pl.tps = tps;
             pl.ns = eff;
             pl.pairs = pairs;
+            best_resident = resident > 0 ? resident : 1;
         }
     }
     if (pl.ns == 0) {
@@ -522,6 +524,7 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
     }
     pl.tiles = tiles;
     pl.lds = mfma_lds_bytes(pl.tps, ngm, a.batch, pl.rt, f32_meta);
+    pl.rounds = (pl.nbands * pl.ns + best_resident - 1) / best_resident;
     return pl;
 }
 

@@ -63,6 +63,7 @@ struct MfmaPlan {
     uint32_t tps = 0;     // K tiles per split
     bool pairs = false;   // 16-bit metadata staged with 32-bit loads
     size_t lds = 0;       // dynamic LDS bytes per workgroup
+    uint32_t rounds = 0;  // rounds of resident workgroups the grid takes
 };
 bool affine_mfma_supported(const AffineArgs &a);
 MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim);

@@ -146,9 +146,13 @@ qmr::RowsPlan forced_rows_plan(const qmr_device *dev, const qmr::AffineArgs &a) 
 }
 
 // One packed-affine product of at most four RHS: the split-K matrix-core
-// kernel where it supports the format, else the vector-ALU kernels. A forced
-// plan (testing hook) of rr > 0 or rr == -1 selects the vector-ALU tilings,
-// rr == -3 the row-owning matrix-core kernel.
+// kernel where it supports the format and its grid fits in one round of
+// resident workgroups; past that (tall matrices such as a vocabulary head,
+// where the split-K kernel's per-workgroup staging and cross-workgroup sums
+// repeat round after round) the row-owning matrix-core kernel; else the
+// vector-ALU kernels. A forced plan (testing hook) of rr > 0 or rr == -1
+// selects the vector-ALU tilings, rr == -3 the row-owning matrix-core
+// kernel, rr == -2 the split-K kernel whatever its rounds.
 hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
     const qmr::GemvPlan f = dev->forced_plan;
     if (f.rr == -3 && qmr::affine_rows_supported(a)) {
@@ -157,6 +161,10 @@ hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
     }
     if ((f.rr == 0 || f.rr == -2 || f.rr == -3) && qmr::affine_mfma_supported(a)) {
         const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, dev->limits);
+        if (f.rr == 0 && pl.rt > 0 && pl.rounds > 1 && qmr::affine_rows_supported(a)) {
+            const qmr::RowsPlan rp = qmr::plan_affine_rows(a, dev->limits);
+            if (rp.rt > 0) return qmr::launch_affine_rows(a, rp, dev->stream);
+        }
         if (pl.rt > 0) {
             ensure_workspace(dev, qmr::affine_mfma_workspace(pl, a), pl.nbands);
             return qmr::launch_affine_mfma(a, pl, dev->ws_partial, dev->ws_counters, dev->stream);
@@ -727,6 +735,14 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
         }
         if ((f.rr == 0 || f.rr == -2 || f.rr == -3) && qmr::affine_mfma_supported(a)) {
             const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, device->limits);
+            if (f.rr == 0 && pl.rt > 0 && pl.rounds > 1 && qmr::affine_rows_supported(a)) {
+                const qmr::RowsPlan rp = qmr::plan_affine_rows(a, device->limits);
+                if (rp.rt > 0) {
+                    if (rr) *rr = -3;
+                    if (ks) *ks = int(rp.j * 10000 + rp.rt * 100 + rp.kw);
+                    return QMR_OK;
+                }
+            }
             if (pl.rt > 0) {
                 // Matrix-core kernel: rr = -2, ks = K splits across workgroups.
                 if (rr) *rr = -2;

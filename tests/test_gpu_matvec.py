@@ -231,6 +231,17 @@ def test_row_kernel_is_deterministic(gpu, rows, cols, batch):
     assert_gate(got[0], want, f"rows {plan} {rows}x{cols} B{batch}")
 
 
+@pytest.mark.parametrize("rows,cols,batch,kind", [(5120, 17408, 1, -2), (17408, 5120, 3, -2),
+                                                  (151936, 5120, 1, -3), (151936, 5120, 3, -3)])
+def test_default_plan_takes_row_owning_kernel_past_one_round(gpu, rows, cols, batch, kind):
+    """The default planner keeps the split-K kernel while its grid fits in
+    one round of resident workgroups (the MLP shapes) and takes the
+    row-owning kernel past that (the vocabulary head)."""
+    gpu.set_gemv_plan(0, 0)
+    plan = gpu.gemv_plan(rows, cols, 4, batch)
+    assert plan[0] == kind, f"{rows}x{cols} B{batch}: expected plan kind {kind}, got {plan}"
+
+
 @pytest.mark.parametrize("rr,name,batch", [(0, "matmul_affine_bf16", 1), (0, "matmul_affine_bf16", 3),
                                            (-3, "matmul_affine_bf16", 2), (0, "matmul_affine_wide_bf16", 100)])
 def test_matrix_core_kernels_read_x_at_4_byte_offsets(gpu, rr, name, batch):
