@@ -20,6 +20,10 @@ events to report the spread.
 The CPU baseline times the FP64 oracle (the reference's per-weight
 dequantise-then-accumulate closure, restated in C) on this host.
 
+BASELINE config 3 (the Q8/g64 F16 5120x5120 projection and the Q4/g64 BF16
+151936x5120 vocabulary head, B=1 and B=3) is reported under "config3" with an
+HBM roofline per case.
+
 BASELINE config 4 (the wide block: 17408x5120 Q4/g64 BF16 times 128 and 256
 FP32 columns) is timed the same way and reported under "wide" with its own
 matrix-core roofline (algorithmic FLOP against the dense f16 peak); it is not
@@ -187,9 +191,49 @@ def bench_wide(gpu: qmr.Gpu, args) -> list:
     return out
 
 
+def bench_config3(gpu: qmr.Gpu, args) -> list:
+    """the Q8/g64 F16-metadata 5120x5120 attention
+    projection and the Q4/g64 BF16 151936x5120 vocabulary head, each at B=1
+    and B=3. Weights rotate over enough copies to exceed the Infinity Cache
+    (10 of the 26 MB projection, 2 of the 440 MB head)."""
+    cases = [("q8_proj", synth.q8_f16_matrix(5120, 5120, synth.DEFAULT_SEED, tag="q8"), 10),
+             ("head", synth.q4_bf16_matrix(*synth.HEAD_SHAPE, synth.DEFAULT_SEED, tag="head"), 2)]
+    out = []
+    for tag, m, copies in cases:
+        mats = [(gpu.upload_bytes(m.w), gpu.upload_bytes(m.s), gpu.upload_bytes(m.b))
+                for _ in range(copies)]
+        suffix = "_f16meta" if m.meta == "f16" else "_bf16"
+        for batch in (1, 3):
+            x = synth.activations(m.cols, batch, synth.DEFAULT_SEED, tag="bench")
+            xb = gpu.upload_f32(x.ravel())
+            ys = [gpu.alloc_f32(batch * m.rows) for _ in range(copies)]
+            bufsets = [[w, s, b, xb, y] for (w, s, b), y in zip(mats, ys)]
+            name = ("matvec_affine" if batch == 1 else "matmul_affine") + suffix
+            params = [m.rows, m.cols, m.bits, m.group] + ([batch] if batch > 1 else [])
+            log(f"bench: {tag} {m.rows}x{m.cols} Q{m.bits} B={batch} ({name})")
+            mean_ms, _, _ = time_kernel(gpu, name, bufsets, params, args.config3_steps, 6)
+            nbytes = synth.algorithmic_bytes(m, batch)
+            gbps = nbytes / (mean_ms * 1e-3) / 1e9
+            plan = gpu.gemv_plan(m.rows, m.cols, m.bits, batch)
+            r = {
+                "shape": f"{m.rows}x{m.cols}", "tag": tag, "bits": m.bits, "metadata": m.meta,
+                "batch": batch, "kernel": hip_kernel(plan), "plan": list(plan),
+                "us_mean": round(mean_ms * 1e3, 2), "algorithmic_bytes": nbytes,
+                "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBS, 4)},
+            }
+            log(f"bench:   {r['us_mean']} us, {r['roofline']['achieved']} GB/s = "
+                f"{100 * r['roofline']['frac']:.1f}% of peak ({r['kernel']})")
+            out.append(r)
+            del bufsets, ys, xb
+        del mats
+    return out
+
+
 def hip_kernel(plan) -> str:
-    """The HIP kernel family the planner picked (plan[0] == -2: matrix cores)."""
-    return "affine_mfma_kernel" if plan[0] == -2 else "affine_gemv_kernel"
+    """The HIP kernel family the planner picked (plan[0]: -2 split-K matrix
+    cores, -3 row-owning matrix cores, otherwise the vector-ALU kernel)."""
+    return {-2: "affine_mfma_kernel", -3: "affine_rows_kernel"}.get(plan[0], "affine_gemv_kernel")
 
 
 def load_traffic(tag: str):
@@ -218,6 +262,9 @@ def main() -> int:
     ap.add_argument("--only-wide", action="store_true",
                     help="time only the config-4 wide block (for profiling runs)")
     ap.add_argument("--wide-steps", type=int, default=30)
+    ap.add_argument("--config3-steps", type=int, default=60)
+    ap.add_argument("--no-config3", action="store_true",
+                    help="skip the config-3 Q8 projection and vocabulary head")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run plain copies of MIB MiB (counter calibration for profiling)")
     args = ap.parse_args()
@@ -278,6 +325,7 @@ def main() -> int:
         print(json.dumps({"wide": wide}), flush=True)
         gpu.close()
         return 0
+    config3 = [] if (args.only_metric or args.no_config3) else bench_config3(gpu, args)
     head = next(r for r in results if r["tag"] == "down" and r["batch"] == 1)
     b3 = next(r for r in results if r["tag"] == "down" and r["batch"] == 3)
     cpu = None
@@ -317,6 +365,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "results": results,
+        "config3": config3,
         "wide": wide,
     }
     print(json.dumps(line), flush=True)
