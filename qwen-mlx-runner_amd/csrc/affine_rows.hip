@@ -419,15 +419,19 @@ RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                 if (lds > lim.max_lds_per_block) continue;
                 const uint32_t nbands = (row_tiles + rt - 1) / rt;
                 const uint32_t n_chunks = (n_entries + kw * j - 1) / (kw * j);
-                // Score: about eight waves per CU, at least one workgroup per
-                // CU, few idle steps (a partial last chunk), staging requested
-                // several entries ahead (J), and staged x shared by several
-                // tiles when the block is wide.
+                // Score: about eight waves per CU, workgroups of about sixteen
+                // waves (more bytes requested per workgroup), at least one
+                // workgroup per CU, few idle steps (a partial last chunk),
+                // staging requested several entries ahead (J), and staged x
+                // shared by several tiles when the block is wide. The weights
+                // were fitted to MI355X timings of every (rt, kw, j) on Q4
+                // and Q8 matrices from 2048x2048 to the 151936x5120 head.
                 const double waves = double(nbands) * rt * kw;
                 const double fill = double(n_entries) / (double(n_chunks) * kw * j);
-                double score = std::fabs(std::log2(waves / (8.0 * cus))) + 4.0 * (1.0 - fill) +
-                               0.25 * a.batch / rt + (j >= 4 ? 0.0 : j == 2 ? 0.5 : 1.0);
-                if (nbands < cus) score += std::log2(cus / nbands);
+                double score = std::fabs(std::log2(waves / (8.0 * cus))) + 1.0 * (1.0 - fill) +
+                               0.25 * a.batch / rt + 0.5 * (j >= 4 ? 0.0 : j == 2 ? 0.5 : 1.0) +
+                               0.25 * std::fabs(std::log2(double(rt * kw) / 16.0));
+                if (nbands < cus) score += 0.5 * std::log2(cus / nbands);
                 if (row_tiles % rt) score += 1.0 - double(row_tiles) / (double(nbands) * rt);
                 if (score < best_score - 1e-9) {
                     best_score = score;

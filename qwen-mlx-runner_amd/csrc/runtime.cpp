@@ -145,14 +145,26 @@ qmr::RowsPlan forced_rows_plan(const qmr_device *dev, const qmr::AffineArgs &a) 
     return qmr::plan_affine_rows(a, dev->limits);
 }
 
+// Whether the default planner hands a split-K plan to the row-owning kernel.
+// Every split-K workgroup pays fixed costs (its metadata staging, the partial
+// store and the band's last-arrival sum) that its K range has to amortise.
+// They repeat round after round when the grid needs more than one round of
+// resident workgroups (tall matrices such as a vocabulary head), and they
+// dominate when a split covers fewer than four K tiles (small matrices, and
+// 8-bit codes, whose rows hold few 128-byte entries): measured on MI355X, a
+// 5120x5120 Q8 projection takes 9-10 us on the row-owning kernel against
+// 11.9 us split 14 ways over 3-tile splits, while the MLP shapes (8-tile
+// splits) stay faster split-K.
+bool rows_preferred(const qmr::MfmaPlan &pl) {
+    return pl.rounds > 1 || (pl.ns > 1 && pl.tps < 4);
+}
+
 // One packed-affine product of at most four RHS: the split-K matrix-core
-// kernel where it supports the format and its grid fits in one round of
-// resident workgroups; past that (tall matrices such as a vocabulary head,
-// where the split-K kernel's per-workgroup staging and cross-workgroup sums
-// repeat round after round) the row-owning matrix-core kernel; else the
-// vector-ALU kernels. A forced plan (testing hook) of rr > 0 or rr == -1
-// selects the vector-ALU tilings, rr == -3 the row-owning matrix-core
-// kernel, rr == -2 the split-K kernel whatever its rounds.
+// kernel where it supports the format, unless rows_preferred() hands the
+// shape to the row-owning matrix-core kernel; else the vector-ALU kernels.
+// A forced plan (testing hook) of rr > 0 or rr == -1 selects the vector-ALU
+// tilings, rr == -3 the row-owning matrix-core kernel, rr == -2 the split-K
+// kernel whatever its shape.
 hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
     const qmr::GemvPlan f = dev->forced_plan;
     if (f.rr == -3 && qmr::affine_rows_supported(a)) {
@@ -161,7 +173,7 @@ hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
     }
     if ((f.rr == 0 || f.rr == -2 || f.rr == -3) && qmr::affine_mfma_supported(a)) {
         const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, dev->limits);
-        if (f.rr == 0 && pl.rt > 0 && pl.rounds > 1 && qmr::affine_rows_supported(a)) {
+        if (f.rr == 0 && pl.rt > 0 && rows_preferred(pl) && qmr::affine_rows_supported(a)) {
             const qmr::RowsPlan rp = qmr::plan_affine_rows(a, dev->limits);
             if (rp.rt > 0) return qmr::launch_affine_rows(a, rp, dev->stream);
         }
@@ -735,7 +747,7 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
         }
         if ((f.rr == 0 || f.rr == -2 || f.rr == -3) && qmr::affine_mfma_supported(a)) {
             const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, device->limits);
-            if (f.rr == 0 && pl.rt > 0 && pl.rounds > 1 && qmr::affine_rows_supported(a)) {
+            if (f.rr == 0 && pl.rt > 0 && rows_preferred(pl) && qmr::affine_rows_supported(a)) {
                 const qmr::RowsPlan rp = qmr::plan_affine_rows(a, device->limits);
                 if (rp.rt > 0) {
                     if (rr) *rr = -3;

@@ -231,14 +231,18 @@ def test_row_kernel_is_deterministic(gpu, rows, cols, batch):
     assert_gate(got[0], want, f"rows {plan} {rows}x{cols} B{batch}")
 
 
-@pytest.mark.parametrize("rows,cols,batch,kind", [(5120, 17408, 1, -2), (17408, 5120, 3, -2),
-                                                  (151936, 5120, 1, -3), (151936, 5120, 3, -3)])
-def test_default_plan_takes_row_owning_kernel_past_one_round(gpu, rows, cols, batch, kind):
+@pytest.mark.parametrize("rows,cols,bits,batch,kind", [
+    (5120, 17408, 4, 1, -2), (17408, 5120, 4, 3, -2), (5120, 5120, 4, 1, -2), (5120, 17408, 8, 1, -2),
+    (151936, 5120, 4, 1, -3), (151936, 5120, 4, 3, -3), (5120, 5120, 8, 1, -3), (5120, 5120, 8, 3, -3),
+    (2048, 2048, 8, 1, -3)])
+def test_default_plan_takes_row_owning_kernel_past_one_round(gpu, rows, cols, bits, batch, kind):
     """The default planner keeps the split-K kernel while its grid fits in
-    one round of resident workgroups (the MLP shapes) and takes the
-    row-owning kernel past that (the vocabulary head)."""
+    one round of resident workgroups and each split covers at least four K
+    tiles (the Q4 and Q8 MLP shapes, a Q4 5120x5120 matrix), and takes the
+    row-owning kernel past one round (the vocabulary head) or for shorter
+    splits (the Q8 5120x5120 projection, a Q8 2048x2048 matrix)."""
     gpu.set_gemv_plan(0, 0)
-    plan = gpu.gemv_plan(rows, cols, 4, batch)
+    plan = gpu.gemv_plan(rows, cols, bits, batch)
     assert plan[0] == kind, f"{rows}x{cols} B{batch}: expected plan kind {kind}, got {plan}"
 
 
