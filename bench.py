@@ -15,7 +15,9 @@ library's stream; their difference over K is the mean launch duration, and
 `value` is the algorithmic bytes of one launch (codes + scales + biases + x +
 y) divided by it. The wall time of that timed region (synchronised on both
 sides) gives ms_per_step. A second pass brackets each launch with its own
-events to report the spread.
+events to report the spread. Before the W warmup launches of each case, about
+1 s of untimed launches lets the GPU clocks settle after the host-side idle
+of building that case's matrix.
 
 The CPU baseline times the FP64 oracle (the reference's per-weight
 dequantise-then-accumulate closure, restated in C) on this host.
@@ -56,12 +58,38 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+SETTLE_MS = 1000.0
+
+
+def settle(gpu: qmr.Gpu, name: str, bufsets, params, threads: int, ms: float) -> None:
+    """Untimed launches until about `ms` of GPU time has run. The clocks ramp
+    up over a few hundred milliseconds of load after the host has kept the
+    GPU idle (as it does while it builds each synthetic matrix): on MI355X
+    the first timed region of the 5120x17408 GEMV read 14.8 us after 50 ms of
+    such launches, 14.1 us after 200 ms and a steady 13.8 us after 1 s; the
+    vocabulary head read 90 us cold against 77 us steady."""
+    cmd = gpu.begin()
+    a = cmd.mark()
+    for k in range(10):
+        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+    b = cmd.mark()
+    cmd.finish()
+    per = max(cmd.elapsed_ms(a, b) / 10, 1e-3)
+    cmd.release()
+    cmd = gpu.begin()
+    for k in range(int(ms / per)):
+        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+    cmd.finish()
+    cmd.release()
+
+
 def time_kernel(gpu: qmr.Gpu, name: str, bufsets, params, steps: int, warmup: int):
     """Back-to-back launch timing (events at both ends of the timed region),
     plus per-launch event brackets for the spread. Returns
     (mean ms per launch back-to-back, wall seconds of that region,
      per-launch bracketed durations in ms)."""
     _, threads = qmr.dispatch_layout(name, params)
+    settle(gpu, name, bufsets, params, threads, SETTLE_MS)
     cmd = gpu.begin()
     for k in range(warmup):
         cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
@@ -341,6 +369,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms_per_case": SETTLE_MS,
         "ms_per_step": head["wall_ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
