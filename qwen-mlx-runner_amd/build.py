@@ -26,6 +26,7 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", f"--offload-arch={ARCH}"]
 
 SOURCES = [
     ("contract.cpp", ["-x", "c++"]),
+    ("checkpoint.cpp", ["-x", "c++"]),
     ("runtime.cpp", ["-x", "hip"]),
     ("affine_gemv.hip", ["-x", "hip"]),
     ("affine_mfma.hip", ["-x", "hip"]),

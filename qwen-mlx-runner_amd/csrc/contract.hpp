@@ -9,6 +9,8 @@
 #include <string>
 #include <vector>
 
+struct qmr_device;
+
 namespace qmr {
 
 // Error carrying the reference's message text; converted to a status code and
@@ -17,6 +19,16 @@ struct Error {
     int code;
     std::string message;
 };
+
+// The C-ABI's thread-local error message (qmr_last_error), for entry points
+// defined outside runtime.cpp: record_error stores `message` and returns
+// `code`; clear_error empties it at the start of a call.
+int record_error(int code, const std::string &message);
+void clear_error();
+
+// Bytes of device memory currently free on the device's GPU (hipMemGetInfo);
+// throws Error on a HIP failure.
+size_t device_free_bytes(const ::qmr_device *device);
 
 enum class BlockMatmulMode : int { Legacy = 0, Shared = 1, MlpR2 = 2 };
 

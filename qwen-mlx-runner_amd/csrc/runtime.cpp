@@ -94,6 +94,24 @@ void check_hip(hipError_t e, const char *what) {
     if (e != hipSuccess) throw Error{QMR_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e)};
 }
 
+}  // namespace
+
+namespace qmr {
+int record_error(int code, const std::string &message) { return set_error(code, message); }
+void clear_error() { g_error.clear(); }
+}  // namespace qmr
+
+namespace qmr {
+size_t device_free_bytes(const ::qmr_device *device) {
+    size_t free_bytes = 0, total = 0;
+    check_hip(hipSetDevice(device->ordinal), "hipSetDevice");
+    check_hip(hipMemGetInfo(&free_bytes, &total), "hipMemGetInfo");
+    return free_bytes;
+}
+}  // namespace qmr
+
+namespace {
+
 bool is_variant(const std::string &v) {
     return v == "packed4" || v == "aligned" || v == "stream";
 }

@@ -43,6 +43,10 @@ EXPORTED_SYMBOLS = (
     "qmr_specialized_matmul", "qmr_parse_block_kernel_mode", "qmr_pack_bf16_exact",
     "qmr_supported_bf16_quantization", "qmr_set_gemv_plan", "qmr_gemv_plan",
     "qmr_last_kernel", "qmr_device_max_lds",
+    # include/qmr_checkpoint.h
+    "qmr_checkpoint_open", "qmr_checkpoint_close", "qmr_checkpoint_tensor_count",
+    "qmr_checkpoint_contains", "qmr_checkpoint_matrix_info", "qmr_checkpoint_matrix",
+    "qmr_checkpoint_dense", "qmr_matrix_load", "qmr_matrix_release",
 )
 
 
@@ -61,6 +65,18 @@ class _Options(C.Structure):
 class _Timing(C.Structure):
     _fields_ = [("cpu_encode_seconds", C.c_double), ("cpu_commit_seconds", C.c_double),
                 ("gpu_seconds", C.c_double), ("completion_wait_seconds", C.c_double)]
+
+
+class _MatrixInfo(C.Structure):
+    _fields_ = [("packed", C.c_int), ("rows", C.c_size_t), ("cols", C.c_size_t),
+                ("bits", C.c_uint32), ("group_size", C.c_size_t), ("dtype", C.c_char * 8),
+                ("metadata_dtype", C.c_char * 8)]
+
+
+class _Matrix(C.Structure):
+    _fields_ = [("weight", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("rows", C.c_size_t), ("cols", C.c_size_t), ("bits", C.c_uint32),
+                ("group", C.c_size_t), ("metadata_bf16", C.c_int)]
 
 
 @dataclass
@@ -133,6 +149,15 @@ def lib() -> C.CDLL:
                                     C.POINTER(C.c_int), C.POINTER(C.c_int)]),
         "qmr_last_kernel": (C.c_char_p, [vp]),
         "qmr_device_max_lds": (sz, [vp]),
+        "qmr_checkpoint_open": (C.c_int, [C.c_char_p, C.POINTER(vp)]),
+        "qmr_checkpoint_close": (None, [vp]),
+        "qmr_checkpoint_tensor_count": (sz, [vp]),
+        "qmr_checkpoint_contains": (C.c_int, [vp, C.c_char_p]),
+        "qmr_checkpoint_matrix_info": (C.c_int, [vp, C.c_char_p, C.POINTER(_MatrixInfo)]),
+        "qmr_checkpoint_matrix": (C.c_int, [vp, C.c_char_p, vp, vp, vp]),
+        "qmr_checkpoint_dense": (C.c_int, [vp, C.c_char_p, vp]),
+        "qmr_matrix_load": (C.c_int, [vp, vp, C.c_char_p, sz, sz, C.POINTER(_Matrix)]),
+        "qmr_matrix_release": (None, [C.POINTER(_Matrix)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -358,6 +383,13 @@ class Gpu:
                                         s.size, so.ctypes.data, bo.ctypes.data)
         return (so, bo) if ok else None
 
+    def metadata_stats(self) -> tuple[int, int]:
+        """Gpu::metadata_stats (src/gpu.rs:491-496): matrices whose metadata was
+        compacted to BF16, and the bytes that saved."""
+        n, saved = C.c_size_t(), C.c_uint64()
+        lib().qmr_metadata_stats(self._h, C.byref(n), C.byref(saved))
+        return n.value, saved.value
+
     # -- buffers (src/gpu.rs:540-589)
     def alloc(self, nbytes: int) -> Buffer:
         h = C.c_void_p()
@@ -407,6 +439,114 @@ class Gpu:
         return self
 
     def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        if _alive:
+            try:
+                self.close()
+            except Exception:
+                pass
+
+
+# ---- checkpoints (include/qmr_checkpoint.h) ----
+
+@dataclass
+class MatrixInfo:
+    """What Checkpoint::matrix (src/weights.rs:292-351) returns, without the data."""
+    packed: bool
+    rows: int
+    cols: int
+    bits: int
+    group_size: int
+    dtype: str
+    metadata_dtype: str
+
+
+@dataclass
+class PackedData:
+    """MatrixData::Packed (src/weights.rs:15-29): words and FP32 metadata."""
+    rows: int
+    cols: int
+    bits: int
+    group_size: int
+    weights: np.ndarray
+    scales: np.ndarray
+    biases: np.ndarray
+
+
+@dataclass
+class DenseData:
+    """MatrixData::Dense: F16 bit patterns, row-major."""
+    rows: int
+    cols: int
+    values: np.ndarray
+
+
+@dataclass
+class Matrix:
+    """A matrix resident on one device (`Matrix`, src/engine.rs:22-31)."""
+    weight: Buffer
+    scales: Optional[Buffer]
+    biases: Optional[Buffer]
+    rows: int
+    cols: int
+    bits: int
+    group: int
+    metadata_bf16: bool
+
+
+class Checkpoint:
+    """Checkpoint (src/weights.rs:47-486): an MLX safetensors checkpoint,
+    memory-mapped and validated when opened."""
+
+    def __init__(self, path: str | os.PathLike):
+        h = C.c_void_p()
+        _check(lib().qmr_checkpoint_open(os.fsencode(os.fspath(path)), C.byref(h)))
+        self._h = h
+
+    def __len__(self) -> int:
+        return int(lib().qmr_checkpoint_tensor_count(self._h))
+
+    def contains(self, name: str) -> bool:
+        return bool(lib().qmr_checkpoint_contains(self._h, name.encode()))
+
+    def matrix_info(self, name: str) -> MatrixInfo:
+        i = _MatrixInfo()
+        _check(lib().qmr_checkpoint_matrix_info(self._h, name.encode(), C.byref(i)))
+        return MatrixInfo(bool(i.packed), i.rows, i.cols, i.bits, i.group_size,
+                          i.dtype.decode(), i.metadata_dtype.decode())
+
+    def matrix(self, name: str) -> PackedData | DenseData:
+        i = self.matrix_info(name)
+        if not i.packed:
+            v = np.empty(i.rows * i.cols, np.uint16)
+            _check(lib().qmr_checkpoint_dense(self._h, name.encode(), v.ctypes.data))
+            return DenseData(i.rows, i.cols, v)
+        w = np.empty(i.rows * i.cols // (32 // i.bits), np.uint32)
+        g = i.rows * i.cols // i.group_size
+        sc, bi = np.empty(g, np.float32), np.empty(g, np.float32)
+        _check(lib().qmr_checkpoint_matrix(self._h, name.encode(), w.ctypes.data, sc.ctypes.data,
+                                           bi.ctypes.data))
+        return PackedData(i.rows, i.cols, i.bits, i.group_size, w, sc, bi)
+
+    def load(self, gpu: "Gpu", name: str, rows: int, cols: int) -> Matrix:
+        """Matrix::load (src/engine.rs:48-135) into `gpu`'s memory."""
+        m = _Matrix()
+        _check(lib().qmr_matrix_load(gpu.handle, self._h, name.encode(), rows, cols, C.byref(m)))
+        own = lambda h: Buffer(h) if h else None  # the Buffer objects release them
+        return Matrix(own(m.weight), own(m.scales), own(m.biases), m.rows, m.cols, m.bits,
+                      m.group, bool(m.metadata_bf16))
+
+    def close(self) -> None:
+        if self._h:
+            lib().qmr_checkpoint_close(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self) -> "Checkpoint":
+        return self
+
+    def __exit__(self, *exc) -> None:
         self.close()
 
     def __del__(self):

@@ -1,6 +1,9 @@
 """Shared input builders and checks for the GPU parity tests."""
 from __future__ import annotations
 
+import json
+import struct
+
 import numpy as np
 
 import oracle
@@ -76,3 +79,30 @@ def run_affine(gpu: qmr.Gpu, name: str, w, s, b, x, rows, cols, bits, group, bat
     params = [rows, cols, bits, group] + ([batch] if name.startswith("matmul") else [])
     gpu.dispatch(name, [wb, sb, bb, xb, yb], params)
     return gpu.read_f32(yb, batch * rows)
+
+
+# ---- safetensors checkpoints written by the tests
+
+def write_tensor_file(path: Path, tensors, metadata=None) -> None:
+    """Safetensors writer in the shape of the reference's test helper
+    (src/weights.rs:759-776): tensors laid out in order, offsets relative to
+    the data section."""
+    header, data = {}, b""
+    if metadata is not None:
+        header["__metadata__"] = metadata
+    for name, dtype, shape, payload in tensors:
+        start = len(data)
+        data += payload
+        header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [start, len(data)]}
+    h = json.dumps(header).encode()
+    path.write_bytes(struct.pack("<Q", len(h)) + h + data)
+
+
+def write_raw(path: Path, header: bytes, data: bytes = b"") -> None:
+    path.write_bytes(struct.pack("<Q", len(header)) + header + data)
+
+
+def write_config(d: Path, **extra) -> None:
+    cfg = {"model_type": "qwen3_5_text", "hidden_size": 8}
+    cfg.update(extra)
+    (d / "config.json").write_text(json.dumps(cfg))
