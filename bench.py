@@ -26,6 +26,9 @@ BASELINE config 3 (the Q8/g64 F16 5120x5120 projection and the Q4/g64 BF16
 151936x5120 vocabulary head, B=1 and B=3) is reported under "config3" with an
 HBM roofline per case.
 
+The checkpoint loader (MLX safetensors to device buffers) is timed on one
+layer's three MLP matrices and reported under "loader" (host-to-device GB/s).
+
 BASELINE config 4 (the wide block: 17408x5120 Q4/g64 BF16 times 128 and 256
 FP32 columns) is timed the same way and reported under "wide" with its own
 matrix-core roofline (algorithmic FLOP against the dense f16 peak); it is not
@@ -258,6 +261,60 @@ def bench_config3(gpu: qmr.Gpu, args) -> list:
     return out
 
 
+PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
+
+
+def bench_loader(args) -> dict:
+    """The checkpoint loader: one layer's three MLP matrices (gate and up
+    17408x5120, down 5120x17408, Q4/g64 with BF16 metadata) written as an MLX
+    safetensors checkpoint in a temporary directory, then opened and loaded
+    into a "bf16" device (qmr_checkpoint_open + qmr_matrix_load, the
+    reference's Checkpoint::open + Matrix::load). The file is in the page
+    cache, as after a first load; the figure is host-to-device throughput."""
+    import shutil
+    import tempfile
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import write_config, write_tensor_file
+
+    d = Path(tempfile.mkdtemp(prefix="qmr_ck_"))
+    try:
+        tensors, shapes = [], {}
+        for proj, key in (("gate_proj", "gate_up"), ("up_proj", "gate_up"), ("down_proj", "down")):
+            rows, cols = synth.MLP_SHAPES[key]
+            m = synth.q4_bf16_matrix(rows, cols, synth.DEFAULT_SEED, tag=proj)
+            name = f"language_model.model.layers.0.mlp.{proj}"
+            tensors += [(name + ".weight", "U32", [rows, cols // 8], m.w.tobytes()),
+                        (name + ".scales", "BF16", [rows, cols // 64], m.s.tobytes()),
+                        (name + ".biases", "BF16", [rows, cols // 64], m.b.tobytes())]
+            shapes[f"model.layers.0.mlp.{proj}"] = (rows, cols)
+        write_config(d, quantization={"bits": 4, "group_size": 64, "mode": "affine"})
+        write_tensor_file(d / "model.safetensors", tensors)
+        del tensors
+        nbytes = (d / "model.safetensors").stat().st_size
+        gpu = qmr.Gpu("aligned", metadata="bf16")
+        times = []
+        for _ in range(args.loader_reps):
+            t = time.perf_counter()
+            with qmr.Checkpoint(d) as cp:
+                loaded = [cp.load(gpu, n, r, c) for n, (r, c) in shapes.items()]
+            times.append(time.perf_counter() - t)
+            assert all(m.metadata_bf16 for m in loaded)
+            del loaded
+        gpu.close()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    med = statistics.median(times)
+    gbps = nbytes / med / 1e9
+    r = {"workload": "3 MLP matrices (2 x 17408x5120 + 5120x17408, Q4/g64 BF16) from one safetensors file",
+         "file_bytes": nbytes, "reps": len(times), "ms_median": round(med * 1e3, 2),
+         "ms_min": round(min(times) * 1e3, 2),
+         "roofline": {"bound": "pcie", "achieved": round(gbps, 2), "peak": PCIE_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(gbps / PCIE_PEAK_GBS, 4)}}
+    log(f"bench: loader {nbytes / 1e6:.1f} MB in {r['ms_median']} ms = {gbps:.2f} GB/s")
+    return r
+
+
 def hip_kernel(plan) -> str:
     """The HIP kernel family the planner picked (plan[0]: -2 split-K matrix
     cores, -3 row-owning matrix cores, otherwise the vector-ALU kernel)."""
@@ -291,6 +348,8 @@ def main() -> int:
                     help="time only the config-4 wide block (for profiling runs)")
     ap.add_argument("--wide-steps", type=int, default=30)
     ap.add_argument("--config3-steps", type=int, default=60)
+    ap.add_argument("--loader-reps", type=int, default=5)
+    ap.add_argument("--no-loader", action="store_true", help="skip the checkpoint-loader timing")
     ap.add_argument("--no-config3", action="store_true",
                     help="skip the config-3 Q8 projection and vocabulary head")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -354,6 +413,7 @@ def main() -> int:
         gpu.close()
         return 0
     config3 = [] if (args.only_metric or args.no_config3) else bench_config3(gpu, args)
+    loader = None if (args.only_metric or args.no_loader) else bench_loader(args)
     head = next(r for r in results if r["tag"] == "down" and r["batch"] == 1)
     b3 = next(r for r in results if r["tag"] == "down" and r["batch"] == 3)
     cpu = None
@@ -395,6 +455,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "results": results,
         "config3": config3,
+        "loader": loader,
         "wide": wide,
     }
     print(json.dumps(line), flush=True)

@@ -672,7 +672,9 @@ struct qmr_checkpoint {
     void quant_values(const std::string &key, const Tensor &t, float *out) const {
         float_values(t, out);
         const size_t n = elements(t);
-        for (size_t i = 0; i < n; ++i) ensure(std::isfinite(out[i]), key + " contains non-finite values");
+        bool finite = true;
+        for (size_t i = 0; i < n; ++i) finite &= std::isfinite(out[i]);
+        ensure(finite, key + " contains non-finite values");
     }
 
     Resolved resolve(const std::string &name) const {
@@ -719,10 +721,10 @@ struct qmr_checkpoint {
         const size_t n = elements(*r.w);
         std::vector<float> v(n);
         float_values(*r.w, v.data());
-        for (size_t i = 0; i < n; ++i) {
-            ensure(std::isfinite(v[i]) && std::fabs(v[i]) <= 65504.0f, "matrix " + r.key + " exceeds F16 range");
-            out[i] = f32_to_f16_rne(v[i]);
-        }
+        bool in_range = true;
+        for (size_t i = 0; i < n; ++i) in_range &= std::fabs(v[i]) <= 65504.0f;  // false for NaN too
+        ensure(in_range, "matrix " + r.key + " exceeds F16 range");
+        for (size_t i = 0; i < n; ++i) out[i] = f32_to_f16_rne(v[i]);
     }
 };
 
@@ -950,6 +952,28 @@ int qmr_matrix_load(qmr_device *device, const qmr_checkpoint *checkpoint, const 
             ensure(v.size() * 2 < qmr::device_free_bytes(device),
                    "model exceeds the device's free memory; use packed 4-bit weights");
             upload(device, v.data(), v.size() * 2, &m.weight);
+        } else if (r.s->dtype == "BF16" && r.b->dtype == "BF16" &&
+                   std::strcmp(qmr_metadata_mode(device), "bf16") == 0 &&
+                   qmr_supported_bf16_quantization(m.bits, m.group)) {
+            // BF16 metadata for a device that keeps BF16: expanding each value
+            // to FP32 and compacting it back (qmr_compact_metadata) returns the
+            // stored bit pattern for every finite value, so the mapped bytes
+            // are uploaded as they are once no value is Inf or NaN.
+            const size_t n = qmr_checkpoint::elements(*r.s);
+            const std::string module = r.key.substr(0, r.key.size() - 7);
+            for (const auto &part : {std::make_pair(r.s, ".scales"), std::make_pair(r.b, ".biases")}) {
+                const unsigned char *p = checkpoint->bytes(*part.first);
+                bool finite = true;
+                for (size_t i = 0; i < n; ++i) finite &= (p[2 * i + 1] & 0x7f) != 0x7f || (p[2 * i] & 0x80) == 0;
+                ensure(finite, module + part.second + " contains non-finite values");
+            }
+            ensure(r.w->length + 2 * n * 2 < qmr::device_free_bytes(device),
+                   "model exceeds the device's free memory; use packed 4-bit weights");
+            upload(device, checkpoint->bytes(*r.w), r.w->length, &m.weight);
+            upload(device, checkpoint->bytes(*r.s), n * 2, &m.scales);
+            upload(device, checkpoint->bytes(*r.b), n * 2, &m.biases);
+            qmr_record_compacted_metadata(device, uint64_t(n) * 2 * 2);
+            m.metadata_bf16 = 1;
         } else {
             const size_t n = qmr_checkpoint::elements(*r.s);
             std::vector<float> s(n), b(n);

@@ -146,3 +146,29 @@ def test_load_rejects_wrong_shape_without_allocating(tmp_path):
             assert gpu.metadata_stats()[0] == 0
     finally:
         gpu.close()
+
+
+@pytest.mark.parametrize("mode", ["bf16", "f32"])
+@pytest.mark.parametrize("bad", [0x7F80, 0xFF80, 0x7FC1, 0xFFFF])
+def test_non_finite_bf16_metadata_is_rejected(tmp_path, mode, bad):
+    """Inf and NaN BF16 scales or biases fail the load on both metadata paths
+    (Checkpoint::quant_values, src/weights.rs:416-425), including the device
+    that would keep the stored BF16 bits."""
+    write_config(tmp_path, quantization={"bits": 4, "group_size": 32})
+    good = np.full(2, 0x3C00, np.uint16)
+    for which in ("scales", "biases"):
+        s, b = good.copy(), good.copy()
+        (s if which == "scales" else b)[1] = bad
+        write_tensor_file(tmp_path / "model.safetensors", [
+            ("model.w.weight", "U32", [2, 4], np.arange(8, dtype=np.uint32).tobytes()),
+            ("model.w.scales", "BF16", [2, 1], s.tobytes()),
+            ("model.w.biases", "BF16", [2, 1], b.tobytes()),
+        ])
+        gpu = qmr.Gpu("aligned", metadata=mode)
+        try:
+            with qmr.Checkpoint(tmp_path) as cp:
+                with pytest.raises(qmr.QmrError, match=f"model.w.{which} contains non-finite values"):
+                    cp.load(gpu, "model.w", 2, 32)
+            assert gpu.metadata_stats()[0] == 0
+        finally:
+            gpu.close()
