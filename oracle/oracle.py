@@ -131,6 +131,45 @@ def dense_f16_f64(w16, x, rows: int, cols: int, batch: int = 1) -> np.ndarray:
     return y
 
 
+# ---- the decoder layer's elementwise steps around the products (FP64) ----
+
+
+def rms_norm_f64(x, w, eps: float) -> np.ndarray:
+    """kernels/qwen.metal:78-86 (rms_norm) per row of x [batch][n]:
+    y = x * w / sqrt(mean(x^2) + eps)."""
+    x = np.asarray(x, np.float64)
+    x2 = x.reshape(-1, x.shape[-1])
+    inv = 1.0 / np.sqrt(np.mean(x2 * x2, axis=1, keepdims=True) + float(eps))
+    return (x2 * inv * np.asarray(w, np.float64)).reshape(x.shape)
+
+
+def swiglu_f64(g, u) -> np.ndarray:
+    """kernels/qwen.metal:32-33,91-94 (swiglu): silu(g) * u, silu(g) = g / (1 + e^-g)."""
+    g = np.asarray(g, np.float64)
+    return g / (1.0 + np.exp(-g)) * np.asarray(u, np.float64)
+
+
+def mlp_gate_up_f64(gate_m, up_m, kind: str, x, norm_w, eps: float, rows: int, cols: int, bits: int,
+                    group: int, batch: int = 1, threads: int = 1) -> np.ndarray:
+    """The decoder MLP's first half (src/engine.rs:748-764): rms_norm, the
+    gate and up products of the normalised x, then swiglu. gate_m and up_m
+    are (w, s, b) triples; the products are the FP64 oracle of matmul_f64
+    applied to the FP64 normalised x rounded to FP32, the precision the
+    reference hands its GEMV."""
+    n = rms_norm_f64(np.asarray(x, np.float32).reshape(batch, cols), norm_w, eps).astype(np.float32)
+    g = matmul_f64(*gate_m, kind, n, rows, cols, bits, group, batch, threads)
+    u = matmul_f64(*up_m, kind, n, rows, cols, bits, group, batch, threads)
+    return swiglu_f64(g, u)
+
+
+def matmul_add_f64(w, s, b, kind: str, x, r, rows: int, cols: int, bits: int, group: int,
+                   batch: int = 1, threads: int = 1) -> np.ndarray:
+    """A product followed by the reference's add (kernels/qwen.metal:87-90,
+    src/engine.rs:765): y = r + W x."""
+    return np.asarray(r, np.float64).ravel() + matmul_f64(w, s, b, kind, x, rows, cols, bits, group, batch,
+                                                          threads)
+
+
 def gate(y_gpu: np.ndarray, y64: np.ndarray) -> tuple[float, float]:
     """(relative L2, max-abs / max|y64|) of a GPU result against the FP64 oracle."""
     y = np.asarray(y_gpu, dtype=np.float64)

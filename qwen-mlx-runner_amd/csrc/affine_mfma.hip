@@ -69,6 +69,7 @@ struct MfmaParams {
     uint32_t rows, cols;
     uint32_t w_bytes, m_bytes;  // extents of the code and metadata views
     uint32_t nbands, ns, tiles, tps;
+    const float *r;  // residual added to y in the final store (may alias y), or null
 };
 
 // Order this wave's earlier global writes before what follows, without the
@@ -298,8 +299,9 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     const bool writer = lg < WRITERS && row_ok;
     if (p.ns == 1) {
         if (writer) {
-            if (t0 < B) p.y[size_t(t0) * p.rows + row] = v0;
-            if (t0 + 1 < B) p.y[size_t(t0 + 1) * p.rows + row] = v1;
+            const size_t o0 = size_t(t0) * p.rows + row, o1 = o0 + p.rows;
+            if (t0 < B) p.y[o0] = p.r ? p.r[o0] + v0 : v0;
+            if (t0 + 1 < B) p.y[o1] = p.r ? p.r[o1] + v1 : v1;
         }
         return;
     }
@@ -338,7 +340,8 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         float v = pv[0];
 #pragma unroll
         for (uint32_t k = 1; k < kMaxSplits; ++k) v += pv[k];
-        p.y[size_t(t) * p.rows + rr] = v;
+        const size_t o = size_t(t) * p.rows + rr;
+        p.y[o] = p.r ? p.r[o] + v : v;
     }
     if (tid == 0) __hip_atomic_store(&p.counters[band], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -553,6 +556,7 @@ hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *pa
     p.b = a.b;
     p.x = a.x;
     p.y = a.y;
+    p.r = a.residual;
     p.partial = partial;
     p.counters = counters;
     p.rows = a.rows;

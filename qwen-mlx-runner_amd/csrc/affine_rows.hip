@@ -73,9 +73,21 @@ struct RowsParams {
     uint32_t n_entries;         // 128-byte entries per row (the last may be partial)
     uint32_t n_chunks;          // ceil(n_entries / (kw * j))
     uint32_t stage_bytes;       // one LDS staging buffer (16-byte multiple)
+    // Fused forms (AffineArgs): the residual added to y, and for the MLP form
+    // the up matrix, the RMS-norm weights and epsilon.
+    const float *r;
+    const uint32_t *w2;
+    const void *s2;
+    const void *b2;
+    const float *norm;
+    float eps;
 };
 
-template <int BITS, int META, int GROUP, int B, bool PAIRS>
+// MODE 0: y = W x (+ residual). MODE 1, the MLP form: the first rt/2 row
+// tiles of a workgroup are gate rows and the last rt/2 the up rows with the
+// same indices, x is staged as x * norm (the RMS norm's weights; its 1/rms
+// factor is applied to the sums), and y = silu(gate) * up.
+template <int BITS, int META, int GROUP, int B, bool PAIRS, int MODE>
 __global__ __launch_bounds__(kMaxWaves * 64) void affine_rows_kernel(RowsParams p) {
     constexpr int NGM = kTileK / GROUP;  // quant groups per tile
     constexpr int SLOTS = 16 / NGM;      // A rows per quant group
@@ -103,8 +115,11 @@ __global__ __launch_bounds__(kMaxWaves * 64) void affine_rows_kernel(RowsParams 
     const uint32_t CT = KW * J * TPE;        // K tiles per chunk
     const uint32_t gpc = CT * NGM;           // quant groups per chunk
     const uint32_t Gp = gpc | 1;             // LDS pitch of a row's staged metadata (odd)
-    const uint32_t row0 = blockIdx.x * p.rt * 16;
-    const uint32_t tile0 = row0 + ti * 16;
+    constexpr bool MLP = MODE == 1;
+    const uint32_t RTH = MLP ? p.rt / 2 : p.rt;  // row tiles per matrix
+    const uint32_t mat = MLP ? uint32_t(__builtin_amdgcn_readfirstlane(int(ti >= RTH))) : 0u;
+    const uint32_t row0 = blockIdx.x * RTH * 16;
+    const uint32_t tile0 = row0 + (ti - mat * RTH) * 16;
 
     // LDS: [staging buffer 0][staging buffer 1][transpose scratch per wave][sums]
     // A staging buffer: A operands [CT][4 m][4 g][2B] u4, Sx [CT][NGM][HALF/2]
@@ -116,14 +131,21 @@ __global__ __launch_bounds__(kMaxWaves * 64) void affine_rows_kernel(RowsParams 
     unsigned char *tw = trans + size_t(wave) * 16 * kTPitch;
     float *red = reinterpret_cast<float *>(trans + size_t(nthr / 64) * 16 * kTPitch);
 
-    const __amdgpu_buffer_rsrc_t wr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(p.w), 0, int(p.w_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t *>(mat ? p.w2 : p.w), 0, int(p.w_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.s), 0, int(p.m_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t br =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.b), 0, int(p.m_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(p.x), 0, int(uint32_t(B) * p.cols * 4u), kRsrcWord3);
+    // MLP form only (the pointers are null otherwise and these go unused).
+    const __amdgpu_buffer_rsrc_t sr2 =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.s2), 0, int(p.m_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t br2 =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.b2), 0, int(p.m_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t nr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p.norm), 0, int(p.cols * 4u), kRsrcWord3);
 
     // ---- Staging of one chunk: loads into registers, then conversion into
     // an LDS buffer. Loads are issued only by waves with work (a wave-uniform
@@ -144,6 +166,12 @@ __global__ __launch_bounds__(kMaxWaves * 64) void affine_rows_kernel(RowsParams 
             const uint32_t it = tid + i * nthr;
             load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), c * CT * kTileK + item_col<B>(it), p.cols,
                     it < items);
+            if constexpr (MLP) {
+                float nv[8];
+                load_x8(nv, nr, 0u, c * CT * kTileK + item_col<B>(it), p.cols, it < items);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xv[i][j] *= nv[j];
+            }
         }
 #pragma unroll
         for (int u = 0; u < kMUnits; ++u) {
@@ -152,13 +180,27 @@ __global__ __launch_bounds__(kMaxWaves * 64) void affine_rows_kernel(RowsParams 
             const uint32_t f = tid + u * nthr;
             const uint32_t rl = f / upr;
             const uint32_t g = c * gpc + (f - rl * upr) * UE;
-            const uint32_t off = (f < units && g < m_pitch) ? ((row0 + rl) * m_pitch + g) * MB : kOut;
+            // MLP form: staged rows RTH*16.. are the up matrix's rows 0...
+            const bool second = MLP && rl >= RTH * 16;
+            const uint32_t mrow = row0 + rl - (second ? RTH * 16 : 0u);
+            const uint32_t off = (f < units && g < m_pitch) ? (mrow * m_pitch + g) * MB : kOut;
+            const uint32_t off1 = second ? kOut : off;
             if constexpr (MB == 4 || PAIRS) {
-                mv_s[u] = __builtin_amdgcn_raw_buffer_load_b32(sr, int(off), 0, 0);
-                mv_b[u] = __builtin_amdgcn_raw_buffer_load_b32(br, int(off), 0, 0);
+                mv_s[u] = __builtin_amdgcn_raw_buffer_load_b32(sr, int(off1), 0, 0);
+                mv_b[u] = __builtin_amdgcn_raw_buffer_load_b32(br, int(off1), 0, 0);
+                if constexpr (MLP) {
+                    const uint32_t off2 = second ? off : kOut;
+                    mv_s[u] |= __builtin_amdgcn_raw_buffer_load_b32(sr2, int(off2), 0, 0);
+                    mv_b[u] |= __builtin_amdgcn_raw_buffer_load_b32(br2, int(off2), 0, 0);
+                }
             } else {
-                mv_s[u] = __builtin_amdgcn_raw_buffer_load_b16(sr, int(off), 0, 0);
-                mv_b[u] = __builtin_amdgcn_raw_buffer_load_b16(br, int(off), 0, 0);
+                mv_s[u] = __builtin_amdgcn_raw_buffer_load_b16(sr, int(off1), 0, 0);
+                mv_b[u] = __builtin_amdgcn_raw_buffer_load_b16(br, int(off1), 0, 0);
+                if constexpr (MLP) {
+                    const uint32_t off2 = second ? off : kOut;
+                    mv_s[u] |= __builtin_amdgcn_raw_buffer_load_b16(sr2, int(off2), 0, 0);
+                    mv_b[u] |= __builtin_amdgcn_raw_buffer_load_b16(br2, int(off2), 0, 0);
+                }
             }
         }
     };
@@ -249,9 +291,35 @@ __global__ __launch_bounds__(kMaxWaves * 64) void affine_rows_kernel(RowsParams 
         issue(ring[j], uint32_t(j));
         __builtin_amdgcn_sched_barrier(0);
     }
+    // MLP form: sum of squares of each x[t] (the RMS norm's statistic),
+    // reduced per wave into the sums area (unused until the epilogue), while
+    // the first weight entries are in flight.
+    if constexpr (MLP) {
+        float sq[B];
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+            sq[t] = 0.f;
+            for (uint32_t k = uint32_t(tid) * 4u; k < p.cols; k += uint32_t(nthr) * 4u) {
+                const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, int((uint32_t(t) * p.cols + k) * 4u), 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sq[t] += __uint_as_float(v[e]) * __uint_as_float(v[e]);
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) sq[t] += __shfl_xor(sq[t], m, 64);
+            if (lane == 0) red[wave * B + t] = sq[t];
+        }
+    }
     stage_store(0);
     if (p.n_chunks > 1) stage_load(1);
     lds_barrier();
+    // 1/rms of this lane's RHS in the epilogue (lane/16), from the per-wave sums.
+    float inv_t = 1.f;
+    if constexpr (MLP) {
+        const int t = (lane >> 4) < B ? (lane >> 4) : 0;
+        float ss = 0.f;
+        for (int wv = 0; wv < nthr / 64; ++wv) ss += red[wv * B + t];
+        inv_t = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
+    }
 
     // ---- This wave's entries i = 0, 1, ... (entry kw + KW*i, chunk i / J).
     // Every wave runs the same number of steps, so the barriers match. ----
@@ -308,24 +376,36 @@ __global__ __launch_bounds__(kMaxWaves * 64) void affine_rows_kernel(RowsParams 
         if (L.t0 + 1 < B) rw[(L.t0 + 1) * 16 + r] = v1;
     }
     __syncthreads();
-    if (kw == 0 && lane < B * 16) {
+    if (kw == 0 && lane < B * 16 && (!MLP || ti < RTH)) {
         const int t = lane >> 4;
         const uint32_t row = tile0 + uint32_t(lane & 15);
         float sum = 0.f;
         for (uint32_t k = 0; k < KW; ++k) sum += red[((ti * KW + k) * B + t) * 16 + (lane & 15)];
-        if (row < p.rows) p.y[size_t(t) * p.rows + row] = sum;
+        if constexpr (MLP) {
+            // The up rows with the same indices sit in tile ti + RTH.
+            float up = 0.f;
+            for (uint32_t k = 0; k < KW; ++k) up += red[(((ti + RTH) * KW + k) * B + t) * 16 + (lane & 15)];
+            const float g = sum * inv_t;
+            sum = g * (1.0f / (1.0f + expf(-g))) * (up * inv_t);
+        }
+        if (row < p.rows) {
+            const size_t o = size_t(t) * p.rows + row;
+            p.y[o] = p.r ? p.r[o] + sum : sum;
+        }
     }
 }
 
 template <int BITS, int META, int GROUP, int B, bool PAIRS>
 hipError_t launch_b(const RowsParams &p, uint32_t nbands, size_t lds, hipStream_t stream) {
-    auto kernel = affine_rows_kernel<BITS, META, GROUP, B, PAIRS>;
-    static size_t configured = 0;
-    if (lds > 65536 && lds > configured) {
+    auto kernel = p.w2 ? affine_rows_kernel<BITS, META, GROUP, B, PAIRS, 1>
+                       : affine_rows_kernel<BITS, META, GROUP, B, PAIRS, 0>;
+    static size_t configured[2] = {0, 0};
+    size_t &done = configured[p.w2 ? 1 : 0];
+    if (lds > 65536 && lds > done) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         if (e != hipSuccess) return e;
-        configured = lds;
+        done = lds;
     }
     hipLaunchKernelGGL(kernel, dim3(nbands), dim3(p.rt * p.kw * 64), lds, stream, p);
     return hipGetLastError();
@@ -389,11 +469,15 @@ size_t rows_lds_bytes(uint32_t kw, uint32_t j, uint32_t rt, uint32_t bits, uint3
 
 bool affine_rows_supported(const AffineArgs &a) { return affine_mfma_supported(a); }
 
-RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_rt,
-                          uint32_t force_kw, uint32_t force_j) {
+namespace {
+
+// The tiling search behind plan_affine_rows and plan_affine_mlp. The MLP form
+// stacks the gate and up tiles of the same rows: twice the row tiles, rt even.
+RowsPlan plan_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_rt, uint32_t force_kw,
+                   uint32_t force_j, bool mlp) {
     RowsPlan best;
     if (!affine_rows_supported(a)) return best;
-    const uint32_t row_tiles = (a.rows + 15) / 16;
+    const uint32_t row_tiles = (a.rows + 15) / 16 * (mlp ? 2 : 1);
     const uint32_t row_bytes = a.cols / 32 * (a.bits * 4);
     const uint32_t n_entries = (row_bytes + 127) / 128;
     const uint32_t ngm = kTileK / a.group;
@@ -404,7 +488,7 @@ RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     double best_score = 1e30;
     for (uint32_t rt = 1; rt <= 8; rt *= 2) {
         for (uint32_t kw = 1; kw <= 16; kw *= 2) {
-            if (rt * kw > uint32_t(kMaxWaves) || rt * kw < 2) continue;
+            if (rt * kw > uint32_t(kMaxWaves) || rt * kw < 2 || (mlp && rt < 2)) continue;
             if (force_rt && (rt != force_rt || kw != force_kw)) continue;
             const uint32_t threads = 64 * rt * kw;
             const uint32_t per_wave = (n_entries + kw - 1) / kw;
@@ -451,6 +535,15 @@ RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     return best;
 }
 
+}  // namespace
+
+RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_rt, uint32_t force_kw,
+                          uint32_t force_j) {
+    return plan_rows(a, lim, force_rt, force_kw, force_j, false);
+}
+
+RowsPlan plan_affine_mlp(const AffineArgs &a, const DeviceLimits &lim) { return plan_rows(a, lim, 0, 0, 0, true); }
+
 hipError_t launch_affine_rows(const AffineArgs &a, const RowsPlan &pl, hipStream_t stream) {
     if (pl.rt == 0) return hipErrorInvalidValue;
     RowsParams p;
@@ -469,6 +562,13 @@ hipError_t launch_affine_rows(const AffineArgs &a, const RowsPlan &pl, hipStream
     p.n_entries = pl.n_entries;
     p.n_chunks = pl.n_chunks;
     p.stage_bytes = uint32_t(pl.stage_bytes);
+    p.r = a.residual;
+    p.w2 = a.up_w;
+    p.s2 = a.up_s;
+    p.b2 = a.up_b;
+    p.norm = a.norm;
+    p.eps = a.eps;
+    if (a.up_w && (pl.rt % 2 != 0 || !a.up_s || !a.up_b || !a.norm)) return hipErrorInvalidValue;
     const int meta = static_cast<int>(a.meta);
     if (a.bits == 4) {
         if (meta == 0) return launch_meta<4, 0>(p, a.group, a.batch, false, pl.nbands, pl.lds, stream);

@@ -4,6 +4,7 @@
 #include "contract.hpp"
 
 #include <climits>
+#include <cmath>
 #include <cstring>
 
 namespace qmr {
@@ -38,6 +39,16 @@ Meta meta_of_name(const std::string &name) {
 bool is_wide_name(const std::string &name) { return starts_with(name, "matmul_affine_wide"); }
 
 bool is_block_name(const std::string &name) { return starts_with(name, "matmul_"); }
+
+bool is_residual_name(const std::string &name) {
+    return name == "matmul_affine_add" || name == "matmul_affine_add_bf16" || name == "matmul_affine_add_f16meta";
+}
+
+bool is_mlp_name(const std::string &name) {
+    return name == "mlp_gate_up_swiglu" || name == "mlp_gate_up_swiglu_bf16" || name == "mlp_gate_up_swiglu_f16meta";
+}
+
+bool is_fused_name(const std::string &name) { return is_residual_name(name) || is_mlp_name(name); }
 
 bool is_affine_matrix_name(const std::string &name) {
     return starts_with(name, "matvec_affine") || starts_with(name, "matmul_affine");
@@ -94,8 +105,10 @@ Layout dispatch_layout(const std::string &name, const uint32_t *p, size_t np) {
         count = 3;
     } else if (name == "matmul_affine" || name == "matmul_affine_bf16" ||
                name == "matmul_affine_f16meta" || name == "matmul_affine_wide" ||
-               name == "matmul_affine_wide_bf16") {
+               name == "matmul_affine_wide_bf16" || is_residual_name(name)) {
         count = 5;
+    } else if (is_mlp_name(name)) {
+        count = 6;
     } else {
         fail("Unknown GPU kernel " + name);
     }
@@ -164,6 +177,31 @@ Layout dispatch_layout(const std::string &name, const uint32_t *p, size_t np) {
         return out;
     }
 
+    // Fused MLP (no reference counterpart): [rows, cols, bits, group, batch,
+    // eps bits]; buffers gate w/s/b, up w/s/b, x [batch][cols], RMS-norm
+    // weights [cols], y [batch][rows].
+    if (is_mlp_name(name)) {
+        positive({0, 1});
+        const size_t batch = n(4);
+        ensure(batch >= 1 && batch <= 4, "Matrix blocks support one through four RHS");
+        const float eps = [&] {
+            float v;
+            std::memcpy(&v, &p[5], 4);
+            return v;
+        }();
+        ensure(std::isfinite(eps) && eps > 0.f, name + ": epsilon must be finite and positive");
+        ensure(supported_bf16_quantization(p[2], n(3)), "Matrix blocks support affine Q4/Q8 groups 32, 64 or 128");
+        ensure(n(1) % n(3) == 0, "Invalid packed matrix alignment");
+        const size_t total = product({n(0), n(1)});
+        size_t metadata, packed_bits;
+        ensure(!mul_overflow(total / n(3), meta_bytes_per, &metadata), "Affine block metadata byte size overflow");
+        ensure(!mul_overflow(total, n(2), &packed_bits), "Packed block byte size overflow");
+        out.sizes = {packed_bits / 8, metadata, metadata, packed_bits / 8, metadata, metadata,
+                     f(product({batch, n(1)})), f(n(1)), f(product({batch, n(0)}))};
+        out.threads = product({n(0), 32});
+        return out;
+    }
+
     // Blocks: matmul_affine*, matmul_f16 (src/gpu.rs:1130-1172).
     positive({0, 1});
     const bool affine = name != "matmul_f16";
@@ -189,6 +227,7 @@ Layout dispatch_layout(const std::string &name, const uint32_t *p, size_t np) {
         out.sizes = {dense};
     }
     out.sizes.push_back(f(product({batch, n(1)})));
+    if (is_residual_name(name)) out.sizes.push_back(f(product({batch, n(0)})));  // residual r
     out.sizes.push_back(f(product({batch, n(0)})));
     out.threads = product({n(0), 32});
     return out;

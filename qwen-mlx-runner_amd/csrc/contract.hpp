@@ -70,5 +70,11 @@ Meta meta_of_name(const std::string &name);
 bool is_affine_matrix_name(const std::string &name);  // matvec/matmul affine family
 bool is_block_name(const std::string &name);          // matmul_affine*, matmul_f16
 bool is_wide_name(const std::string &name);           // matmul_affine_wide*
+// Fused names with no reference counterpart: matmul_affine_add[_bf16|_f16meta]
+// (y = r + W x) and mlp_gate_up_swiglu[_bf16|_f16meta] (RMS norm, gate and up
+// products and SwiGLU in one launch).
+bool is_residual_name(const std::string &name);
+bool is_mlp_name(const std::string &name);
+bool is_fused_name(const std::string &name);
 
 }  // namespace qmr

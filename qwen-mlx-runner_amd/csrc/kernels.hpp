@@ -22,6 +22,17 @@ struct AffineArgs {
     float *y;
     uint32_t rows, cols, bits, group, batch;
     Meta meta;
+    // Fused forms (null when unused).
+    //  - residual: y = residual + W x, added in the final store (may alias y).
+    //  - MLP (up_w set): w/s/b are the gate matrix and up_w/up_s/up_b the up
+    //    matrix of the same shape and format; x[t] is RMS-normalised with the
+    //    `norm` weights and `eps`, and y[t] = silu(gate x) * (up x).
+    const float *residual = nullptr;
+    const uint32_t *up_w = nullptr;
+    const void *up_s = nullptr;
+    const void *up_b = nullptr;
+    const float *norm = nullptr;
+    float eps = 0.f;
 };
 
 // Tiling of the GEMV/block kernel. A workgroup has 8 half-wave row slots;
@@ -90,6 +101,9 @@ struct RowsPlan {
 bool affine_rows_supported(const AffineArgs &a);
 // force_rt/force_kw (both nonzero) pin the workgroup shape and force_j the
 // chunk depth; zeros leave the choice to the planner.
+// The MLP form's tiling: gate and up tiles of the same rows in one workgroup
+// (even rt, the first rt/2 tiles from the gate matrix).
+RowsPlan plan_affine_mlp(const AffineArgs &a, const DeviceLimits &lim);
 RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_rt = 0,
                           uint32_t force_kw = 0, uint32_t force_j = 0);
 hipError_t launch_affine_rows(const AffineArgs &a, const RowsPlan &pl, hipStream_t stream);

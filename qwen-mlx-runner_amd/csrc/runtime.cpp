@@ -200,6 +200,8 @@ hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
             return qmr::launch_affine_mfma(a, pl, dev->ws_partial, dev->ws_counters, dev->stream);
         }
     }
+    // The vector-ALU kernels have no fused epilogue.
+    ensure(a.residual == nullptr, "fused product needs a matrix-core kernel", QMR_ERR_UNSUPPORTED);
     return qmr::launch_affine_gemv(a, f.rr < -1 ? qmr::GemvPlan{} : f, dev->limits, dev->stream);
 }
 
@@ -546,12 +548,17 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
             }
         }
         // A matrix-block output is never an input; a copy's views are
-        // disjoint or identical (src/gpu.rs:658-672).
-        if (qmr::starts_with(name, "matmul_") || name == "copy_f32") {
+        // disjoint or identical (src/gpu.rs:658-672). The fused forms follow
+        // the block rule, except that y may be exactly the residual's view
+        // (the in-place x += W a of a decoder layer).
+        const bool fused = qmr::is_fused_name(name);
+        ensure(!dev->reference || !fused, "Fused dispatch is unavailable in reference mode");
+        if (qmr::starts_with(name, "matmul_") || name == "copy_f32" || fused) {
             const size_t out = nbuffers - 1;
             for (size_t i = 0; i < out; ++i) {
                 if (buffers[i] == buffers[out]) {
-                    const bool identical_copy = name == "copy_f32" && off(i) == off(out);
+                    const bool identical_copy = (name == "copy_f32" || (qmr::is_residual_name(name) && i == 4)) &&
+                                                off(i) == off(out);
                     ensure(identical_copy ||
                                !qmr::ranges_overlap(off(i), layout.sizes[i], off(out), layout.sizes[out]),
                            name + ": output overlaps input buffer " + std::to_string(i));
@@ -571,7 +578,7 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
         const char *label = nullptr;
         const bool aligned_variant = dev->gemv_variant == "aligned";
         const bool wide = qmr::is_wide_name(name);
-        if (qmr::starts_with(name, "matmul_") && !wide && meta != qmr::Meta::F16) {
+        if (qmr::starts_with(name, "matmul_") && !wide && !fused && meta != qmr::Meta::F16) {
             label = qmr::specialized_matmul(
                 name, params,
                 aligned_variant && off(0) % 8 == 0 && off(name == "matmul_f16" ? 1 : 3) % 16 == 0,
@@ -623,8 +630,40 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                                       reinterpret_cast<const float *>(ptr(1)),
                                       reinterpret_cast<float *>(ptr(2)), params[0], params[1],
                                       batch, dev->stream);
+        } else if (fused) {
+            qmr::AffineArgs a{};
+            a.rows = params[0];
+            a.cols = params[1];
+            a.bits = params[2];
+            a.group = params[3];
+            a.batch = params[4];
+            a.meta = meta;
+            a.w = reinterpret_cast<const uint32_t *>(ptr(0));
+            a.s = ptr(1);
+            a.b = ptr(2);
+            if (qmr::is_mlp_name(name)) {
+                a.up_w = reinterpret_cast<const uint32_t *>(ptr(3));
+                a.up_s = ptr(4);
+                a.up_b = ptr(5);
+                a.x = reinterpret_cast<const float *>(ptr(6));
+                a.norm = reinterpret_cast<const float *>(ptr(7));
+                a.y = reinterpret_cast<float *>(ptr(8));
+                std::memcpy(&a.eps, &params[5], 4);
+                ensure(qmr::affine_rows_supported(a), name + ": no fused kernel for this format",
+                       QMR_ERR_UNSUPPORTED);
+                const qmr::RowsPlan pl = qmr::plan_affine_mlp(a, dev->limits);
+                ensure(pl.rt > 0, name + ": no fused tiling for this shape", QMR_ERR_UNSUPPORTED);
+                e = qmr::launch_affine_rows(a, pl, dev->stream);
+            } else {
+                a.x = reinterpret_cast<const float *>(ptr(3));
+                a.residual = reinterpret_cast<const float *>(ptr(4));
+                a.y = reinterpret_cast<float *>(ptr(5));
+                ensure(qmr::affine_mfma_supported(a), name + ": no fused kernel for this format",
+                       QMR_ERR_UNSUPPORTED);
+                e = launch_product(dev, a);
+            }
         } else {
-            qmr::AffineArgs a;
+            qmr::AffineArgs a{};
             a.w = reinterpret_cast<const uint32_t *>(ptr(0));
             a.s = ptr(1);
             a.b = ptr(2);

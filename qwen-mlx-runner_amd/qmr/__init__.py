@@ -185,10 +185,10 @@ def _s(v: Optional[str]) -> Optional[bytes]:
 
 def dispatch_layout(name: str, params: Sequence[int]) -> tuple[list[int], int]:
     """dispatch_layout (src/gpu.rs:1041-1294) for the matrix kernels."""
-    sizes = (C.c_size_t * 8)()
+    sizes = (C.c_size_t * 16)()
     n = C.c_size_t()
     threads = C.c_size_t()
-    _check(lib().qmr_dispatch_layout(name.encode(), _u32(params), len(params), sizes, 8,
+    _check(lib().qmr_dispatch_layout(name.encode(), _u32(params), len(params), sizes, 16,
                                      C.byref(n), C.byref(threads)))
     return [sizes[i] for i in range(n.value)], threads.value
 

@@ -200,6 +200,30 @@ def test_added_names_layouts():
         err(qmr.dispatch_layout, "matmul_affine_wide", [16, 512, 4, 64, batch])
 
 
+def test_fused_names_layouts():
+    """The fused forms (no reference counterpart): the residual product takes
+    the block's buffers plus r [batch][rows] before y; the MLP form takes the
+    gate and up matrices, x, the RMS-norm weights and y, with a finite
+    positive epsilon as its sixth word."""
+    assert qmr.dispatch_layout("matmul_affine_add_bf16", [3, 128, 4, 64, 2]) == \
+        ([192, 12, 12, 1024, 24, 24], 96)
+    assert qmr.dispatch_layout("matmul_affine_add", [5120, 17408, 4, 64, 1]) == \
+        ([44564480, 5570560, 5570560, 4 * 17408, 4 * 5120, 4 * 5120], 5120 * 32)
+    eps = int(np.float32(1e-6).view(np.uint32))
+    sizes, threads = qmr.dispatch_layout("mlp_gate_up_swiglu_bf16", [17408, 5120, 4, 64, 3, eps])
+    w, m = 17408 * 5120 // 2, 17408 * 80 * 2
+    assert sizes == [w, m, m, w, m, m, 4 * 3 * 5120, 4 * 5120, 4 * 3 * 17408] and threads == 17408 * 32
+    assert qmr.dispatch_layout("mlp_gate_up_swiglu", [16, 256, 8, 32, 1, eps])[0][1] == 16 * 8 * 4
+    for bad in (0, int(np.float32(-1e-6).view(np.uint32)), 0x7F800000, 0x7FC00000):
+        with pytest.raises(qmr.QmrError, match="epsilon must be finite and positive"):
+            qmr.dispatch_layout("mlp_gate_up_swiglu_f16meta", [16, 256, 4, 64, 1, bad])
+    for batch in (0, 5):
+        err(qmr.dispatch_layout, "mlp_gate_up_swiglu_bf16", [16, 256, 4, 64, batch, eps])
+        err(qmr.dispatch_layout, "matmul_affine_add_bf16", [16, 256, 4, 64, batch])
+    err(qmr.dispatch_layout, "mlp_gate_up_swiglu_bf16", [16, 256, 4, 48, 1, eps])
+    err(qmr.dispatch_layout, "mlp_gate_up_swiglu_bf16", [16, 256, 4, 64, 1])
+
+
 # src/gpu/metadata.rs:24-71 through the library's own routine.
 def test_pack_bf16_exact_patterns_and_supported_formats():
     patterns = np.array([0x00000000, 0x80000000, 0x3FC00000, 0xC0200000, 0x00010000, 0x80010000,

@@ -266,3 +266,78 @@ def test_config0_golden_vector():
     assert np.array_equal(m.b[:16], z["b_head"]) and np.array_equal(x.ravel()[:16], z["x_head"])
     y = oracle.matmul_f64(m.w, m.s, m.b, "bf16", x, 1024, 1024, 4, 64)
     assert np.array_equal(y, z["y64"])
+
+
+# ------------------------------------- the decoder layer's elementwise steps
+
+
+def test_rms_norm_swiglu_and_add_kats():
+    """src/gpu.rs:1785-1791 (rms_norm), 1822-1825 (swiglu, add)."""
+    eps = float(np.float32(1e-6))
+    d = np.sqrt(12.5 + eps)
+    np.testing.assert_allclose(oracle.rms_norm_f64([3.0, 4.0], [2.0, 1.0], eps), [6 / d, 4 / d], rtol=1e-15)
+    np.testing.assert_allclose(oracle.swiglu_f64([0.0, 1.0], [3.0, 4.0]), [0.0, 4 / (1 + np.exp(-1.0))],
+                               rtol=1e-15)
+    # The Q4 known answer (src/gpu.rs:1637-1657) with a residual: [48, 14] + [0, 1].
+    w = np.array([0x76543210, 0xFEDCBA98], np.uint32)
+    y = oracle.matmul_add_f64(w, np.array([2.0, 0.5], np.float32), np.array([-1.0, -4.0], np.float32), "f32",
+                              np.ones(8, np.float32), [0.0, 1.0], 2, 8, 4, 8)
+    assert y.tolist() == [48.0, 15.0]
+
+
+def test_rms_norm_and_silu_identities():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 257))
+    w = rng.uniform(0.5, 2.0, 257)
+    # Scale invariance as eps -> 0, and unit RMS for unit weights.
+    np.testing.assert_allclose(oracle.rms_norm_f64(7.5 * x, w, 1e-300), oracle.rms_norm_f64(x, w, 1e-300),
+                               rtol=1e-13)
+    y = oracle.rms_norm_f64(x, np.ones(257), 1e-300)
+    np.testing.assert_allclose(np.sqrt(np.mean(y * y, axis=1)), 1.0, rtol=1e-13)
+    # eps enters under the root: mean(y^2) = m / (m + eps) for unit weights.
+    m = np.mean(x * x, axis=1)
+    y = oracle.rms_norm_f64(x, np.ones(257), 0.25)
+    np.testing.assert_allclose(np.mean(y * y, axis=1), m / (m + 0.25), rtol=1e-13)
+    # silu(g) - silu(-g) = g; silu(0) = 0; silu(g) -> g for large g.
+    g = rng.standard_normal(1000) * 6
+    one = np.ones_like(g)
+    np.testing.assert_allclose(oracle.swiglu_f64(g, one) - oracle.swiglu_f64(-g, one), g, rtol=1e-12, atol=1e-15)
+    assert oracle.swiglu_f64([0.0], [5.0]).tolist() == [0.0]
+    np.testing.assert_allclose(oracle.swiglu_f64([40.0], [1.0]), [40.0], rtol=1e-15)
+
+
+def test_mlp_oracle_matches_a_scalar_brute_force():
+    """mlp_gate_up_f64 against loops over the reference's per-weight formula
+    (tests/quantized.rs:39-51) and the elementwise kernels, on a 5x64 Q4/g32
+    case with two RHS."""
+    import math
+
+    rng = np.random.default_rng(11)
+    rows, cols, group, batch, eps = 5, 64, 32, 2, 1e-5
+    mats = []
+    for _ in range(2):
+        w = rng.integers(0, 2**32, rows * cols // 8, dtype=np.uint64).astype(np.uint32)
+        s = rng.uniform(0.01, 0.1, rows * cols // group).astype(np.float32)
+        b = (-8 * s + rng.normal(0, 1e-3, s.size)).astype(np.float32)
+        mats.append((w, s, b))
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    got = oracle.mlp_gate_up_f64(mats[0], mats[1], "f32", x, nw, eps, rows, cols, 4, group, batch)
+
+    def product(m, v, r):
+        w, s, b = m
+        acc = 0.0
+        for c in range(cols):
+            q = (int(w[r * (cols // 8) + c // 8]) >> (4 * (c % 8))) & 15
+            gi = r * (cols // group) + c // group
+            acc += (q * float(s[gi]) + float(b[gi])) * float(v[c])
+        return acc
+
+    for t in range(batch):
+        ms = sum(float(v) * float(v) for v in x[t]) / cols
+        inv = 1.0 / math.sqrt(ms + eps)
+        n = [float(np.float32(float(x[t, c]) * inv * float(nw[c]))) for c in range(cols)]
+        for r in range(rows):
+            g, u = product(mats[0], n, r), product(mats[1], n, r)
+            want = g / (1.0 + math.exp(-g)) * u
+            assert abs(got[t * rows + r] - want) <= 1e-12 * max(1.0, abs(want)), (t, r)
