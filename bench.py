@@ -26,6 +26,10 @@ BASELINE config 3 (the Q8/g64 F16 5120x5120 projection and the Q4/g64 BF16
 151936x5120 vocabulary head, B=1 and B=3) is reported under "config3" with an
 HBM roofline per case.
 
+One decoder layer's MLP in the fused forms (RMS norm + gate + up + SwiGLU in
+one launch, down + residual add in a second) is reported under "mlp", beside
+the three plain products timed alone.
+
 The checkpoint loader (MLX safetensors to device buffers) is timed on one
 layer's three MLP matrices and reported under "loader" (host-to-device GB/s).
 
@@ -261,6 +265,87 @@ def bench_config3(gpu: qmr.Gpu, args) -> list:
     return out
 
 
+def bench_mlp(gpu: qmr.Gpu, args) -> list:
+    """One decoder layer's MLP with the fused forms: mlp_gate_up_swiglu_bf16
+    (RMS norm, gate and up 17408x5120, SwiGLU: one launch) then
+    matmul_affine_add_bf16 (down 5120x17408 plus the residual add, in place),
+    at B=1 and B=3. The reference runs the same layer as seven launches
+    (src/engine.rs:748-765); beside the fused pair this times the three
+    plain products alone (matvec/matmul_affine_bf16), which the unfused
+    sequence needs on top of its four elementwise launches."""
+    ku, kd = synth.MLP_SHAPES["gate_up"], synth.MLP_SHAPES["down"]
+    copies = 4
+    mats = {}
+    for tag, (rows, cols) in (("gate", ku), ("up", ku), ("down", kd)):
+        m = synth.q4_bf16_matrix(rows, cols, synth.DEFAULT_SEED, tag=tag)
+        mats[tag] = [(gpu.upload_bytes(m.w), gpu.upload_bytes(m.s), gpu.upload_bytes(m.b)) for _ in range(copies)]
+        nbytes_w = m.w.nbytes + m.s.nbytes + m.b.nbytes
+    eps_bits = int(np.float32(1e-6).view(np.uint32))
+    hidden, inter = ku[1], ku[0]
+    norm = gpu.upload_f32(np.random.default_rng(1).uniform(0.5, 1.5, hidden).astype(np.float32))
+    out = []
+    for batch in (1, 3):
+        x = gpu.upload_f32(synth.activations(hidden, batch, synth.DEFAULT_SEED, tag="mlp").ravel())
+        act = gpu.alloc_f32(batch * inter)
+        resid = gpu.upload_f32(np.zeros(batch * hidden, np.float32))
+        up_sets = [[*mats["gate"][k], *mats["up"][k], x, norm, act] for k in range(copies)]
+        dn_sets = [[*mats["down"][k], act, resid, resid] for k in range(copies)]
+        up_params = [inter, hidden, 4, 64, batch, eps_bits]
+        dn_params = [hidden, inter, 4, 64, batch]
+        _, up_threads = qmr.dispatch_layout("mlp_gate_up_swiglu_bf16", up_params)
+        _, dn_threads = qmr.dispatch_layout("matmul_affine_add_bf16", dn_params)
+        settle(gpu, "mlp_gate_up_swiglu_bf16", up_sets, up_params, up_threads, SETTLE_MS)
+        cmd = gpu.begin()
+        for k in range(5):
+            cmd.encode("mlp_gate_up_swiglu_bf16", up_sets[k % copies], up_params, up_threads, 128)
+            cmd.encode("matmul_affine_add_bf16", dn_sets[k % copies], dn_params, dn_threads, 128)
+        cmd.finish()
+        cmd.release()
+        cmd = gpu.begin()
+        a = cmd.mark()
+        for k in range(args.mlp_steps):
+            cmd.encode("mlp_gate_up_swiglu_bf16", up_sets[k % copies], up_params, up_threads, 128)
+            cmd.encode("matmul_affine_add_bf16", dn_sets[k % copies], dn_params, dn_threads, 128)
+        b = cmd.mark()
+        cmd.finish()
+        layer_ms = cmd.elapsed_ms(a, b) / args.mlp_steps
+        cmd.release()
+        # The three plain products alone, back to back, for comparison.
+        name = "matvec_affine_bf16" if batch == 1 else "matmul_affine_bf16"
+        extra = [] if batch == 1 else [batch]
+        xi = gpu.upload_f32(np.zeros(batch * inter, np.float32))
+        yg, yu, yd = gpu.alloc_f32(batch * inter), gpu.alloc_f32(batch * inter), gpu.alloc_f32(batch * hidden)
+        seq = []
+        for k in range(copies):
+            seq.append((name, [*mats["gate"][k], x, yg], [inter, hidden, 4, 64] + extra))
+            seq.append((name, [*mats["up"][k], x, yu], [inter, hidden, 4, 64] + extra))
+            seq.append((name, [*mats["down"][k], xi, yd], [hidden, inter, 4, 64] + extra))
+        thr = [qmr.dispatch_layout(n, p_)[1] for n, _, p_ in seq]
+        cmd = gpu.begin()
+        a = cmd.mark()
+        for k in range(args.mlp_steps):
+            for j in range(3):
+                n, bufs, p_ = seq[(3 * k + j) % len(seq)]
+                cmd.encode(n, bufs, p_, thr[(3 * k + j) % len(seq)], 128)
+        b = cmd.mark()
+        cmd.finish()
+        plain_ms = cmd.elapsed_ms(a, b) / args.mlp_steps
+        cmd.release()
+        nbytes = 3 * nbytes_w + 4 * batch * (hidden + inter + inter + hidden + hidden) + 4 * hidden
+        gbps = nbytes / (layer_ms * 1e-3) / 1e9
+        r = {"workload": "decoder MLP, 27B shapes, Q4/g64 BF16", "batch": batch, "launches": 2,
+             "us_layer": round(layer_ms * 1e3, 2), "us_three_plain_products": round(plain_ms * 1e3, 2),
+             "algorithmic_bytes": nbytes,
+             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbps / HBM_PEAK_GBS, 4)}}
+        log(f"bench: fused MLP B={batch}: {r['us_layer']} us per layer in 2 launches "
+            f"({r['roofline']['achieved']} GB/s, {100 * r['roofline']['frac']:.1f}% of peak); "
+            f"the 3 plain products alone {r['us_three_plain_products']} us")
+        out.append(r)
+    del mats
+    return out
+
+
 PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
 
 
@@ -349,6 +434,8 @@ def main() -> int:
     ap.add_argument("--wide-steps", type=int, default=30)
     ap.add_argument("--config3-steps", type=int, default=60)
     ap.add_argument("--loader-reps", type=int, default=5)
+    ap.add_argument("--mlp-steps", type=int, default=100)
+    ap.add_argument("--no-mlp", action="store_true", help="skip the fused decoder-MLP timing")
     ap.add_argument("--no-loader", action="store_true", help="skip the checkpoint-loader timing")
     ap.add_argument("--no-config3", action="store_true",
                     help="skip the config-3 Q8 projection and vocabulary head")
@@ -413,6 +500,7 @@ def main() -> int:
         gpu.close()
         return 0
     config3 = [] if (args.only_metric or args.no_config3) else bench_config3(gpu, args)
+    mlp = [] if (args.only_metric or args.no_mlp) else bench_mlp(gpu, args)
     loader = None if (args.only_metric or args.no_loader) else bench_loader(args)
     head = next(r for r in results if r["tag"] == "down" and r["batch"] == 1)
     b3 = next(r for r in results if r["tag"] == "down" and r["batch"] == 3)
@@ -455,6 +543,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "results": results,
         "config3": config3,
+        "mlp": mlp,
         "loader": loader,
         "wide": wide,
     }

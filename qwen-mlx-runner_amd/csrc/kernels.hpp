@@ -103,7 +103,8 @@ bool affine_rows_supported(const AffineArgs &a);
 // chunk depth; zeros leave the choice to the planner.
 // The MLP form's tiling: gate and up tiles of the same rows in one workgroup
 // (even rt, the first rt/2 tiles from the gate matrix).
-RowsPlan plan_affine_mlp(const AffineArgs &a, const DeviceLimits &lim);
+RowsPlan plan_affine_mlp(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_rt = 0,
+                         uint32_t force_kw = 0, uint32_t force_j = 0);
 RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_rt = 0,
                           uint32_t force_kw = 0, uint32_t force_j = 0);
 hipError_t launch_affine_rows(const AffineArgs &a, const RowsPlan &pl, hipStream_t stream);

@@ -651,7 +651,14 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                 std::memcpy(&a.eps, &params[5], 4);
                 ensure(qmr::affine_rows_supported(a), name + ": no fused kernel for this format",
                        QMR_ERR_UNSUPPORTED);
-                const qmr::RowsPlan pl = qmr::plan_affine_mlp(a, dev->limits);
+                // The tuning hook's row-owning shape (rr == -3, ks = j*10000 +
+                // rt*100 + kw) applies to the MLP form too.
+                const qmr::GemvPlan f = dev->forced_plan;
+                const qmr::RowsPlan pl =
+                    f.rr == -3 && f.ks > 0
+                        ? qmr::plan_affine_mlp(a, dev->limits, uint32_t(f.ks / 100 % 100), uint32_t(f.ks % 100),
+                                               uint32_t(f.ks / 10000))
+                        : qmr::plan_affine_mlp(a, dev->limits);
                 ensure(pl.rt > 0, name + ": no fused tiling for this shape", QMR_ERR_UNSUPPORTED);
                 e = qmr::launch_affine_rows(a, pl, dev->stream);
             } else {
