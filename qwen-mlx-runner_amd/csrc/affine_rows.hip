@@ -30,11 +30,14 @@
 //   - End: the KW partial sums of a row are added in LDS in wave order and
 //     written to y. There is no workspace, no atomic and no synchronisation
 //     between workgroups, and results do not depend on timing.
-// Status: opt-in (tuning hook rr = -3); the planner uses affine_mfma.hip.
-// On the MLP shapes it measures 15-16 us against the split-K kernel's 14-15:
-// with only rows/16 tiles (320 for 5120 rows) and two entries in flight per
-// wave, too few bytes are in flight to cover HBM latency, and the per-chunk
-// staging and tile products sit on each wave's critical path.
+// Use: the default where the split-K kernel's per-workgroup costs are not
+// amortised (grids past one round of resident workgroups, such as a
+// vocabulary head, and splits under four K tiles, such as a Q8 5120x5120
+// projection), the fused MLP form (MODE 1 below) always, and the tuning
+// hook rr = -3. On the MLP shapes the split-K kernel stays faster (14-15 us
+// against 15-16): with rows/16 tiles (320 for 5120 rows) and two entries in
+// flight per wave, fewer bytes are in flight to cover HBM latency, and the
+// per-chunk staging and tile products sit on each wave's critical path.
 //
 // Load order per wave: memory counters retire in issue order, so waiting for
 // a load also waits for every load issued before it. The staging loads of
