@@ -13,6 +13,7 @@
 #include <cstdint>
 
 #include "kernels.hpp"
+#include "mfma_common.hpp"
 
 namespace qmr {
 namespace {
@@ -98,6 +99,84 @@ __global__ __launch_bounds__(256) void dense_f16_kernel(const uint16_t *__restri
     if (lane == 0) y[size_t(t) * rows + row] = v;
 }
 
+// Dense F16 weights times token-major FP32 x, streaming form for cols % 8 == 0
+// and matrices under 2 GB: one wave per R rows, each lane taking 8
+// consecutive columns per 512-column step as one 16-byte weight load per row
+// (buffer loads; rows past the matrix read as zeros). The x slice of a step
+// is loaded once and used for the R rows, and every RHS uses the same
+// weight registers, so the matrix is read once whatever B. Two steps are
+// requested before the first is used.
+template <int B, int R>
+__global__ __launch_bounds__(256) void dense_f16_stream_kernel(const uint16_t *__restrict__ w,
+                                                               const float *__restrict__ x,
+                                                               float *__restrict__ y, uint32_t rows,
+                                                               uint32_t cols, uint32_t w_bytes) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * R;
+    const uint32_t lane = threadIdx.x & 63;
+    if (row0 >= rows) return;  // the whole wave
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(w), 0, int(w_bytes), mfma::kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(x), 0, int(uint32_t(B) * cols * 4u), mfma::kRsrcWord3);
+    float acc[R][B];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int t = 0; t < B; ++t) acc[i][t] = 0.f;
+    auto load_w = [&](v4u (&wv)[R], uint32_t c) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const uint32_t off = (c < cols && row0 + i < rows) ? ((row0 + i) * cols + c) * 2u : mfma::kOut;
+            wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, int(off), 0, 0);
+        }
+    };
+    auto use = [&](const v4u (&wv)[R], uint32_t c) {
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+            const uint32_t xo = c < cols ? (uint32_t(t) * cols + c) * 4u : mfma::kOut;
+            const v4u xa = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo), 0, 0);
+            const v4u xb = __builtin_amdgcn_raw_buffer_load_b128(xr, int(xo + 16u), 0, 0);
+            float xv[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xv[j] = __uint_as_float(xa[j]);
+                xv[4 + j] = __uint_as_float(xb[j]);
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // Through a scalar: a bit cast of the vector element
+                    // itself reads the vector's first dword.
+                    const uint32_t d = wv[i][j];
+                    const h2v h = __builtin_bit_cast(h2v, d);
+                    acc[i][t] = __builtin_fmaf(float(h.x), xv[2 * j], acc[i][t]);
+                    acc[i][t] = __builtin_fmaf(float(h.y), xv[2 * j + 1], acc[i][t]);
+                }
+            }
+        }
+    };
+    const uint32_t steps = (cols + 511) / 512;
+    v4u w0[R], w1[R];
+    load_w(w0, lane * 8u);
+    for (uint32_t st = 0; st < steps; st += 2) {
+        const uint32_t c0 = st * 512u + lane * 8u;
+        load_w(w1, c0 + 512u);
+        use(w0, c0);
+        load_w(w0, c0 + 1024u);
+        use(w1, c0 + 512u);
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+            const float v = wave_sum(acc[i][t]);
+            if (lane == 0 && row0 + i < rows) y[size_t(t) * rows + row0 + i] = v;
+        }
+}
+
 __global__ __launch_bounds__(256) void embed_f16_kernel(const uint16_t *__restrict__ w,
                                                         uint32_t row, uint32_t cols,
                                                         float *__restrict__ y) {
@@ -126,6 +205,19 @@ hipError_t launch_embed_affine(const uint32_t *w, const void *s, const void *b, 
 
 hipError_t launch_dense_f16(const uint16_t *w, const float *x, float *y, uint32_t rows,
                             uint32_t cols, uint32_t batch, hipStream_t stream) {
+    constexpr uint32_t R = 4;
+    const uint64_t w_bytes = uint64_t(rows) * cols * 2;
+    if (cols % 8 == 0 && w_bytes < (1ull << 31) && uint64_t(batch) * cols * 4 < (1ull << 31) && batch >= 1 &&
+        batch <= 4) {
+        const uint32_t blocks = (rows + 4 * R - 1) / (4 * R);
+        switch (batch) {
+            case 1: hipLaunchKernelGGL((dense_f16_stream_kernel<1, R>), dim3(blocks), dim3(256), 0, stream, w, x, y, rows, cols, uint32_t(w_bytes)); break;
+            case 2: hipLaunchKernelGGL((dense_f16_stream_kernel<2, R>), dim3(blocks), dim3(256), 0, stream, w, x, y, rows, cols, uint32_t(w_bytes)); break;
+            case 3: hipLaunchKernelGGL((dense_f16_stream_kernel<3, R>), dim3(blocks), dim3(256), 0, stream, w, x, y, rows, cols, uint32_t(w_bytes)); break;
+            default: hipLaunchKernelGGL((dense_f16_stream_kernel<4, R>), dim3(blocks), dim3(256), 0, stream, w, x, y, rows, cols, uint32_t(w_bytes)); break;
+        }
+        return hipGetLastError();
+    }
     const uint64_t waves = uint64_t(rows) * batch;
     const uint64_t blocks = (waves * 64 + 255) / 256;
     hipLaunchKernelGGL(dense_f16_kernel, dim3(uint32_t(blocks)), dim3(256), 0, stream, w, x, y,

@@ -277,3 +277,24 @@ def test_matrix_core_kernels_read_x_at_4_byte_offsets(gpu, rr, name, batch):
         gpu.set_gemv_plan(0, 0)
     assert got[0] == 12345.0 and got[batch * rows + 1] == 12345.0
     assert_gate(got[1:batch * rows + 1], want, f"{name} B{batch} x at a 4-byte offset")
+
+
+@pytest.mark.parametrize("rows,cols,batch", [
+    (5120, 17408, 1), (17408, 5120, 3), (301, 4104, 2), (1000, 8, 4), (77, 1001, 1), (33, 512, 4)])
+def test_dense_f16_products_at_scale(gpu, rows, cols, batch):
+    """matvec_f16 / matmul_f16 (kernels/qwen.metal:48-57,
+    kernels/matmul_block.metal:213-248) against the FP64 oracle: the
+    streaming kernel (cols % 8 == 0, any row tail, 1-4 RHS) and the simple
+    kernel (cols % 8 != 0)."""
+    rng = np.random.default_rng(rows * 3 + cols + batch)
+    w16 = rng.standard_normal(rows * cols).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    wb = gpu.upload_bytes(w16)
+    xb = gpu.upload_f32(x.ravel())
+    yb = gpu.upload_f32(np.full(batch * rows + 1, 7.0, np.float32))
+    name = "matvec_f16" if batch == 1 else "matmul_f16"
+    gpu.dispatch(name, [wb, xb, yb], [rows, cols] + ([batch] if batch > 1 else []))
+    got = gpu.read_f32(yb, batch * rows + 1)
+    assert got[-1] == 7.0, "wrote past y"
+    want = oracle.dense_f16_f64(w16, x, rows, cols, batch)
+    assert_gate(got[:-1], want, f"dense {rows}x{cols} B{batch}")
