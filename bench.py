@@ -30,6 +30,9 @@ One decoder layer's MLP in the fused forms (RMS norm + gate + up + SwiGLU in
 one launch, down + residual add in a second) is reported under "mlp", beside
 the three plain products timed alone.
 
+Dense F16 products (matvec_f16 / matmul_f16) at the MLP shapes are reported
+under "dense_f16".
+
 The checkpoint loader (MLX safetensors to device buffers) is timed on one
 layer's three MLP matrices and reported under "loader" (host-to-device GB/s).
 
@@ -346,6 +349,37 @@ def bench_mlp(gpu: qmr.Gpu, args) -> list:
     return out
 
 
+def bench_dense(gpu: qmr.Gpu, args) -> list:
+    """Dense F16 products at the 27B MLP shapes (matvec_f16 / matmul_f16,
+    kernels/qwen.metal:48-57, kernels/matmul_block.metal:213-248), for
+    checkpoints without quantisation: 178 MB of F16 weights, 3 rotating
+    copies, B=1 and B=3."""
+    out = []
+    for tag in ("down", "gate_up"):
+        rows, cols = synth.MLP_SHAPES[tag]
+        w16 = np.random.default_rng(7).standard_normal(rows * cols).astype(np.float16).view(np.uint16)
+        ws = [gpu.upload_bytes(w16) for _ in range(3)]
+        del w16
+        for batch in (1, 3):
+            xb = gpu.upload_f32(synth.activations(cols, batch, synth.DEFAULT_SEED, tag="dense").ravel())
+            ys = [gpu.alloc_f32(batch * rows) for _ in ws]
+            name = "matvec_f16" if batch == 1 else "matmul_f16"
+            params = [rows, cols] + ([batch] if batch > 1 else [])
+            mean_ms, _, _ = time_kernel(gpu, name, [[w, xb, y] for w, y in zip(ws, ys)], params,
+                                        args.config3_steps, 6)
+            nbytes = rows * cols * 2 + 4 * batch * (rows + cols)
+            gbps = nbytes / (mean_ms * 1e-3) / 1e9
+            r = {"shape": f"{rows}x{cols}", "batch": batch, "name": name, "us_mean": round(mean_ms * 1e3, 2),
+                 "algorithmic_bytes": nbytes,
+                 "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(gbps / HBM_PEAK_GBS, 4)}}
+            log(f"bench: dense F16 {rows}x{cols} B={batch}: {r['us_mean']} us, {r['roofline']['achieved']} GB/s "
+                f"= {100 * r['roofline']['frac']:.1f}% of peak")
+            out.append(r)
+        del ws
+    return out
+
+
 PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
 
 
@@ -357,10 +391,25 @@ def bench_loader(args) -> dict:
     reference's Checkpoint::open + Matrix::load). The file is in the page
     cache, as after a first load; the figure is host-to-device throughput."""
     import shutil
+    import struct
     import tempfile
 
-    sys.path.insert(0, str(ROOT / "tests"))
-    from helpers import write_config, write_tensor_file
+    def write_tensor_file(path: Path, tensors) -> None:
+        # safetensors: 8-byte header length, JSON header, data section.
+        header, data = {}, []
+        pos = 0
+        for name, dtype, shape, payload in tensors:
+            header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [pos, pos + len(payload)]}
+            data.append(payload)
+            pos += len(payload)
+        h = json.dumps(header).encode()
+        with open(path, "wb") as f:
+            f.write(struct.pack("<Q", len(h)) + h)
+            for payload in data:
+                f.write(payload)
+
+    def write_config(d: Path, **extra) -> None:
+        (d / "config.json").write_text(json.dumps({"model_type": "qwen3_5_text", **extra}))
 
     d = Path(tempfile.mkdtemp(prefix="qmr_ck_"))
     try:
@@ -436,6 +485,7 @@ def main() -> int:
     ap.add_argument("--loader-reps", type=int, default=5)
     ap.add_argument("--mlp-steps", type=int, default=100)
     ap.add_argument("--no-mlp", action="store_true", help="skip the fused decoder-MLP timing")
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense F16 timing")
     ap.add_argument("--no-loader", action="store_true", help="skip the checkpoint-loader timing")
     ap.add_argument("--no-config3", action="store_true",
                     help="skip the config-3 Q8 projection and vocabulary head")
@@ -501,6 +551,7 @@ def main() -> int:
         return 0
     config3 = [] if (args.only_metric or args.no_config3) else bench_config3(gpu, args)
     mlp = [] if (args.only_metric or args.no_mlp) else bench_mlp(gpu, args)
+    dense = [] if (args.only_metric or args.no_dense) else bench_dense(gpu, args)
     loader = None if (args.only_metric or args.no_loader) else bench_loader(args)
     head = next(r for r in results if r["tag"] == "down" and r["batch"] == 1)
     b3 = next(r for r in results if r["tag"] == "down" and r["batch"] == 3)
@@ -544,6 +595,7 @@ def main() -> int:
         "results": results,
         "config3": config3,
         "mlp": mlp,
+        "dense_f16": dense,
         "loader": loader,
         "wide": wide,
     }
