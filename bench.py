@@ -469,6 +469,7 @@ def load_traffic(tag: str):
 
 
 def main() -> int:
+    global SETTLE_MS
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
@@ -482,6 +483,8 @@ def main() -> int:
                     help="time only the config-4 wide block (for profiling runs)")
     ap.add_argument("--wide-steps", type=int, default=30)
     ap.add_argument("--config3-steps", type=int, default=60)
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed launches before each case, in ms of GPU time (clock ramp)")
     ap.add_argument("--loader-reps", type=int, default=5)
     ap.add_argument("--mlp-steps", type=int, default=100)
     ap.add_argument("--no-mlp", action="store_true", help="skip the fused decoder-MLP timing")
@@ -492,6 +495,7 @@ def main() -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run plain copies of MIB MiB (counter calibration for profiling)")
     args = ap.parse_args()
+    SETTLE_MS = args.settle_ms
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the hot path is "
               f"single-GPU; multi-GPU sharding is design-only)", file=sys.stderr)
