@@ -70,6 +70,14 @@ struct MfmaParams {
     uint32_t w_bytes, m_bytes;  // extents of the code and metadata views
     uint32_t nbands, ns, tiles, tps;
     const float *r;  // residual added to y in the final store (may alias y), or null
+    // Fused MLP (w2 set): blocks nbands*ns.. take the up matrix (w2/s2/b2);
+    // x is staged as x * norm; the last workgroup of a band adds both
+    // matrices' partials and writes silu(gate/rms) * (up/rms).
+    const uint32_t *w2;
+    const void *s2;
+    const void *b2;
+    const float *norm;
+    float eps;
 };
 
 // Order this wave's earlier global writes before what follows, without the
@@ -103,8 +111,12 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     const int r = lane & 15;
     const int lg = lane >> 4;
     const uint32_t RT = uint32_t(nthr) >> 6;
-    const uint32_t band = blockIdx.x % p.nbands;
-    const uint32_t split = blockIdx.x / p.nbands;
+    const bool mlp = p.w2 != nullptr;
+    const uint32_t nmat = mlp ? 2u : 1u;
+    const uint32_t mat = mlp ? blockIdx.x / (p.nbands * p.ns) : 0u;
+    const uint32_t bid = blockIdx.x - mat * p.nbands * p.ns;
+    const uint32_t band = bid % p.nbands;
+    const uint32_t split = bid / p.nbands;
     const uint32_t T0 = split * p.tps;
     const uint32_t T1 = min(T0 + p.tps, p.tiles);
     const uint32_t nT = T1 - T0;
@@ -121,12 +133,12 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
 
     const uint32_t tile0 = band_row0 + wave * 16;
 
-    const __amdgpu_buffer_rsrc_t wr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(p.w), 0, int(p.w_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t *>(mat ? p.w2 : p.w), 0, int(p.w_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.s), 0, int(p.m_bytes), kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(mat ? p.s2 : p.s), 0, int(p.m_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t br =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.b), 0, int(p.m_bytes), kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(mat ? p.b2 : p.b), 0, int(p.m_bytes), kRsrcWord3);
 
     // ---- 1. Metadata of the band's rows over this K range (to LDS below). ----
     // Rows past the matrix read zeros through the buffer range check.
@@ -170,6 +182,14 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         if (wave_base + i * nthr >= items) continue;
         const uint32_t it = tid + i * nthr;
         load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), T0 * kTileK + item_col<B>(it), p.cols, it < items);
+        if (mlp) {
+            const __amdgpu_buffer_rsrc_t nr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(p.norm), 0, int(p.cols * 4u), kRsrcWord3);
+            float nv[8];
+            load_x8(nv, nr, 0u, T0 * kTileK + item_col<B>(it), p.cols, it < items);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xv[i][j] *= nv[j];
+        }
     }
 
     // ---- 3. The first P entries of codes, requested in ring order. ----
@@ -297,7 +317,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     combine_slots<GROUP>(acc, v0, v1);
     constexpr int WRITERS = 4 / NGM;  // lane groups holding distinct RHS pairs
     const bool writer = lg < WRITERS && row_ok;
-    if (p.ns == 1) {
+    if (p.ns == 1 && !mlp) {
         if (writer) {
             const size_t o0 = size_t(t0) * p.rows + row, o1 = o0 + p.rows;
             if (t0 < B) p.y[o0] = p.r ? p.r[o0] + v0 : v0;
@@ -307,7 +327,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     }
     // Split K: publish this split's partial sums; the last workgroup of the
     // band to arrive adds the ns partials in split order.
-    float *part = p.partial + size_t(split) * B * p.rows;
+    float *part = p.partial + size_t(mat * p.ns + split) * B * p.rows;
     if (writer) {
         if (t0 < B) __hip_atomic_store(part + size_t(t0) * p.rows + row, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (t0 + 1 < B)
@@ -317,13 +337,41 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     __syncthreads();
     if (tid == 0) {
         const uint32_t prev = __hip_atomic_fetch_add(&p.counters[band], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *ldsLast = prev == p.ns - 1 ? 1 : 0;
+        *ldsLast = prev == nmat * p.ns - 1 ? 1 : 0;
     }
     __syncthreads();
     if (*ldsLast == 0) return;
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     const uint32_t band_rows = RT * 16;
+    // MLP: 1/rms of each x[t] (the staged x carried the norm weights only),
+    // from sum(x^2) over all columns, reduced through LDS (the operand area
+    // is free once every wave has left the main loop).
+    float inv[B];
+#pragma unroll
+    for (int t = 0; t < B; ++t) inv[t] = 1.f;
+    if (mlp) {
+        float *sq = reinterpret_cast<float *>(lds);
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+            float v = 0.f;
+            for (uint32_t k = uint32_t(tid) * 4u; k < p.cols; k += uint32_t(nthr) * 4u) {
+                const u4 q = __builtin_amdgcn_raw_buffer_load_b128(xr, int((uint32_t(t) * p.cols + k) * 4u), 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v += __uint_as_float(q[e]) * __uint_as_float(q[e]);
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+            if (lane == 0) sq[wave * B + t] = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+            float ss = 0.f;
+            for (uint32_t wv = 0; wv < RT; ++wv) ss += sq[wv * B + t];
+            inv[t] = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
+        }
+    }
     for (uint32_t i = tid; i < band_rows * B; i += nthr) {
         const uint32_t t = i / band_rows;
         const uint32_t rr = band_row0 + i % band_rows;
@@ -341,7 +389,25 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
 #pragma unroll
         for (uint32_t k = 1; k < kMaxSplits; ++k) v += pv[k];
         const size_t o = size_t(t) * p.rows + rr;
-        p.y[o] = p.r ? p.r[o] + v : v;
+        if (mlp) {
+            // The up matrix's partials follow the gate's ns blocks.
+            const float *pu = p.partial + size_t(p.ns) * stride + size_t(t) * p.rows + rr;
+#pragma unroll
+            for (uint32_t k = 0; k < kMaxSplits; ++k) {
+                pv[k] = k < p.ns ? __hip_atomic_load(pu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+                pu += stride;
+            }
+            float u = pv[0];
+#pragma unroll
+            for (uint32_t k = 1; k < kMaxSplits; ++k) u += pv[k];
+            float it = inv[0];
+#pragma unroll
+            for (int tt = 1; tt < B; ++tt) it = uint32_t(tt) == t ? inv[tt] : it;
+            const float g = v * it;
+            p.y[o] = g * (1.0f / (1.0f + expf(-g))) * (u * it);
+        } else {
+            p.y[o] = p.r ? p.r[o] + v : v;
+        }
     }
     if (tid == 0) __hip_atomic_store(&p.counters[band], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -358,7 +424,7 @@ hipError_t launch_b(const MfmaParams &p, uint32_t rt, size_t lds, hipStream_t st
         if (e != hipSuccess) return e;
         configured = lds;
     }
-    hipLaunchKernelGGL(kernel, dim3(p.nbands * p.ns), dim3(rt * 64), lds, stream, p);
+    hipLaunchKernelGGL(kernel, dim3(p.nbands * p.ns * (p.w2 ? 2u : 1u)), dim3(rt * 64), lds, stream, p);
     return hipGetLastError();
 }
 
@@ -510,9 +576,12 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
         if (lds > lim.max_lds_per_block) continue;
         const uint32_t resident = resident_per_cu(instance(a, pairs), pl.rt * 64, lds) * cus;
         const double target = std::min(20.0, double(resident / cus) * pl.rt) * cus;
-        const double waves = double(pl.nbands) * pl.rt * eff;
+        // The fused MLP form runs the gate and up matrices in one grid.
+        const uint32_t nmat = a.up_w ? 2u : 1u;
+        const double waves = double(pl.nbands) * pl.rt * eff * nmat;
         double score = std::fabs(std::log(waves / target)) + 2.0 * std::log(double(tps) * eff / double(tiles));
-        if (pl.nbands * eff > resident) score += 10.0 * std::ceil(double(pl.nbands * eff) / resident);
+        if (pl.nbands * eff * nmat > resident)
+            score += 10.0 * std::ceil(double(pl.nbands * eff * nmat) / resident);
         if (score < best - 1e-9) {
             best = score;
             pl.tps = tps;
@@ -527,7 +596,7 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
     }
     pl.tiles = tiles;
     pl.lds = mfma_lds_bytes(pl.tps, ngm, a.batch, pl.rt, f32_meta);
-    pl.rounds = (pl.nbands * pl.ns + best_resident - 1) / best_resident;
+    pl.rounds = (pl.nbands * pl.ns * (a.up_w ? 2u : 1u) + best_resident - 1) / best_resident;
     return pl;
 }
 
@@ -544,8 +613,10 @@ bool affine_mfma_supported(const AffineArgs &a) {
 }
 
 size_t affine_mfma_workspace(const MfmaPlan &pl, const AffineArgs &a) {
-    if (pl.ns <= 1) return 0;
-    return size_t(pl.ns) * a.batch * a.rows * sizeof(float);
+    // The fused MLP form always publishes partials (gate and up meet in the
+    // band's last workgroup), one set per matrix.
+    if (pl.ns <= 1 && !a.up_w) return 0;
+    return size_t(a.up_w ? 2 : 1) * pl.ns * a.batch * a.rows * sizeof(float);
 }
 
 hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *partial,
@@ -557,6 +628,11 @@ hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *pa
     p.x = a.x;
     p.y = a.y;
     p.r = a.residual;
+    p.w2 = a.up_w;
+    p.s2 = a.up_s;
+    p.b2 = a.up_b;
+    p.norm = a.norm;
+    p.eps = a.eps;
     p.partial = partial;
     p.counters = counters;
     p.rows = a.rows;

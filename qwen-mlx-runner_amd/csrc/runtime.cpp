@@ -651,16 +651,26 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                 std::memcpy(&a.eps, &params[5], 4);
                 ensure(qmr::affine_rows_supported(a), name + ": no fused kernel for this format",
                        QMR_ERR_UNSUPPORTED);
-                // The tuning hook's row-owning shape (rr == -3, ks = j*10000 +
-                // rt*100 + kw) applies to the MLP form too.
+                // The split-K kernel (measured at 17408x5120: 26.1 us at B=1
+                // and 30.4 at B=3 against 29.4 and 35.5 for the row-owning
+                // MLP mode, although both matrices' grid takes two rounds of
+                // resident workgroups); the row-owning kernel's MLP mode when
+                // the tuning hook asks for it (rr == -3, ks = j*10000 +
+                // rt*100 + kw) or split-K has no plan.
                 const qmr::GemvPlan f = dev->forced_plan;
-                const qmr::RowsPlan pl =
-                    f.rr == -3 && f.ks > 0
-                        ? qmr::plan_affine_mlp(a, dev->limits, uint32_t(f.ks / 100 % 100), uint32_t(f.ks % 100),
-                                               uint32_t(f.ks / 10000))
-                        : qmr::plan_affine_mlp(a, dev->limits);
-                ensure(pl.rt > 0, name + ": no fused tiling for this shape", QMR_ERR_UNSUPPORTED);
-                e = qmr::launch_affine_rows(a, pl, dev->stream);
+                const qmr::MfmaPlan mp = qmr::plan_affine_mfma(a, dev->limits);
+                if (f.rr != -3 && mp.rt > 0) {
+                    ensure_workspace(dev, qmr::affine_mfma_workspace(mp, a), mp.nbands);
+                    e = qmr::launch_affine_mfma(a, mp, dev->ws_partial, dev->ws_counters, dev->stream);
+                } else {
+                    const qmr::RowsPlan pl =
+                        f.rr == -3 && f.ks > 0
+                            ? qmr::plan_affine_mlp(a, dev->limits, uint32_t(f.ks / 100 % 100), uint32_t(f.ks % 100),
+                                                   uint32_t(f.ks / 10000))
+                            : qmr::plan_affine_mlp(a, dev->limits);
+                    ensure(pl.rt > 0, name + ": no fused tiling for this shape", QMR_ERR_UNSUPPORTED);
+                    e = qmr::launch_affine_rows(a, pl, dev->stream);
+                }
             } else {
                 a.x = reinterpret_cast<const float *>(ptr(3));
                 a.residual = reinterpret_cast<const float *>(ptr(4));

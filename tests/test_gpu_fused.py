@@ -56,17 +56,24 @@ def _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind):
     (64, 2048, 4, 128, 4, "bf16"),     # group 128, four RHS
     (24, 4096, 8, 32, 2, "bf16"),      # fewer rows than one tile pair
 ])
-def test_mlp_gate_up_swiglu_matches_unfused_oracle(gpu, rows, cols, bits, group, batch, kind):
+@pytest.mark.parametrize("rr", [0, -2, -3])
+def test_mlp_gate_up_swiglu_matches_unfused_oracle(gpu, rr, rows, cols, bits, group, batch, kind):
+    """Default plan, the split-K kernel forced (rr -2) and the row-owning
+    kernel's MLP mode forced (rr -3)."""
     rng = np.random.default_rng(rows + 7 * cols + batch)
     gate_m = _matrix(rng, rows, cols, bits, group, kind)
     up_m = _matrix(rng, rows, cols, bits, group, kind)
     x = rng.standard_normal((batch, cols)).astype(np.float32) * 3
     nw = rng.uniform(0.2, 1.8, cols).astype(np.float32)
-    got = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind)
     want = oracle.mlp_gate_up_f64(gate_m, up_m, kind, x, nw, EPS, rows, cols, bits, group, batch, 8)
-    assert_gate(got, want, f"mlp {rows}x{cols} Q{bits}/g{group} {kind} B{batch}")
-    again = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind)
-    assert np.array_equal(again.view(np.uint32), got.view(np.uint32)), "launches differ"
+    gpu.set_gemv_plan(rr, 0)
+    try:
+        got = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind)
+        assert_gate(got, want, f"mlp {rows}x{cols} Q{bits}/g{group} {kind} B{batch} rr={rr}")
+        again = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind)
+        assert np.array_equal(again.view(np.uint32), got.view(np.uint32)), "launches differ"
+    finally:
+        gpu.set_gemv_plan(0, 0)
 
 
 def test_mlp_rms_statistic_covers_every_column_and_rhs(gpu):
