@@ -862,8 +862,10 @@ void release_matrix(qmr_matrix *m) {
 }
 
 void upload(qmr_device *device, const void *data, size_t bytes, qmr_buffer **out) {
-    if (qmr_buffer_upload(device, data, bytes, out) != QMR_OK)
-        throw Error{QMR_ERR_DEVICE, qmr_last_error()};
+    // Large arrays (the codes) go through the pinned staging path.
+    const int rc = bytes >= (size_t(32) << 20) ? qmr::upload_staged(device, data, bytes, out)
+                                               : qmr_buffer_upload(device, data, bytes, out);
+    if (rc != QMR_OK) throw Error{QMR_ERR_DEVICE, qmr_last_error()};
 }
 
 }  // namespace

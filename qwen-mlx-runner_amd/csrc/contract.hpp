@@ -10,6 +10,7 @@
 #include <vector>
 
 struct qmr_device;
+struct qmr_buffer;
 
 namespace qmr {
 
@@ -29,6 +30,11 @@ void clear_error();
 // Bytes of device memory currently free on the device's GPU (hipMemGetInfo);
 // throws Error on a HIP failure.
 size_t device_free_bytes(const ::qmr_device *device);
+
+// Uploads `bytes` from a large pageable source (a mapped checkpoint shard)
+// into a new device buffer through pinned staging buffers filled by several
+// host threads; returns QMR_OK or an error status with qmr_last_error() set.
+int upload_staged(::qmr_device *device, const void *src, size_t bytes, ::qmr_buffer **out);
 
 enum class BlockMatmulMode : int { Legacy = 0, Shared = 1, MlpR2 = 2 };
 

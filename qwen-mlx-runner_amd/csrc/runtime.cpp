@@ -9,6 +9,7 @@
 #include <chrono>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/qmr.h"
@@ -44,6 +45,9 @@ struct qmr_device {
     // Workspace of the wide-block kernel: the activation images.
     unsigned char *ws_wide = nullptr;
     size_t ws_wide_bytes = 0;
+    // Pinned staging ring of qmr::upload_staged (allocated on first use).
+    void *pin[2] = {nullptr, nullptr};
+    hipEvent_t pin_done[2] = {nullptr, nullptr};
 };
 
 struct qmr_buffer {
@@ -102,6 +106,61 @@ void clear_error() { g_error.clear(); }
 }  // namespace qmr
 
 namespace qmr {
+
+// Host-to-device copy of a large pageable source through the device's two
+// pinned staging buffers: host threads fill one buffer with the next chunk
+// while the DMA engine drains the other on the device's stream.
+int upload_staged(::qmr_device *device, const void *src, size_t bytes, ::qmr_buffer **out) {
+    constexpr size_t kChunk = size_t(16) << 20;
+    constexpr unsigned kThreads = 8;
+    return guarded([&]() -> int {
+        ensure(device && src && out, "upload_staged: null argument");
+        *out = nullptr;
+        ensure(bytes <= device->max_alloc, "GPU allocation " + std::to_string(bytes) +
+                                               " exceeds device buffer limit " + std::to_string(device->max_alloc));
+        check_hip(hipSetDevice(device->ordinal), "hipSetDevice");
+        for (int i = 0; i < 2; ++i) {
+            if (!device->pin[i]) check_hip(hipHostMalloc(&device->pin[i], kChunk, hipHostMallocDefault), "hipHostMalloc");
+            if (!device->pin_done[i])
+                check_hip(hipEventCreateWithFlags(&device->pin_done[i], hipEventDisableTiming), "hipEventCreate");
+        }
+        void *dst = nullptr;
+        check_hip(hipMalloc(&dst, bytes > 0 ? bytes : 4), "hipMalloc");
+        hipError_t e = hipSuccess;
+        const auto *from = static_cast<const unsigned char *>(src);
+        for (size_t k = 0, pos = 0; pos < bytes && e == hipSuccess; ++k, pos += kChunk) {
+            const int slot = int(k & 1);
+            const size_t len = bytes - pos < kChunk ? bytes - pos : kChunk;
+            if (k >= 2) e = hipEventSynchronize(device->pin_done[slot]);  // its previous chunk has landed
+            if (e != hipSuccess) break;
+            auto *stage = static_cast<unsigned char *>(device->pin[slot]);
+            const size_t part = (len + kThreads - 1) / kThreads;
+            std::vector<std::thread> workers;
+            for (unsigned t = 1; t < kThreads && t * part < len; ++t)
+                workers.emplace_back([=] {
+                    std::memcpy(stage + t * part, from + pos + t * part, std::min(part, len - t * part));
+                });
+            std::memcpy(stage, from + pos, std::min(part, len));
+            for (auto &w : workers) w.join();
+            e = hipMemcpyAsync(static_cast<unsigned char *>(dst) + pos, stage, len, hipMemcpyHostToDevice,
+                               device->stream);
+            if (e == hipSuccess) e = hipEventRecord(device->pin_done[slot], device->stream);
+        }
+        if (e == hipSuccess) e = hipStreamSynchronize(device->stream);
+        if (e != hipSuccess) {
+            hipStreamSynchronize(device->stream);
+            hipFree(dst);
+            check_hip(e, "staged upload");
+        }
+        auto *b = new ::qmr_buffer();
+        b->ordinal = device->ordinal;
+        b->ptr = dst;
+        b->length = bytes;
+        *out = b;
+        return QMR_OK;
+    });
+}
+
 size_t device_free_bytes(const ::qmr_device *device) {
     size_t free_bytes = 0, total = 0;
     check_hip(hipSetDevice(device->ordinal), "hipSetDevice");
@@ -270,6 +329,10 @@ void qmr_device_close(qmr_device *device) {
     if (device->ws_partial) hipFree(device->ws_partial);
     if (device->ws_wide) hipFree(device->ws_wide);
     if (device->ws_counters) hipFree(device->ws_counters);
+    for (int i = 0; i < 2; ++i) {
+        if (device->pin[i]) hipHostFree(device->pin[i]);
+        if (device->pin_done[i]) hipEventDestroy(device->pin_done[i]);
+    }
     delete device;
 }
 
