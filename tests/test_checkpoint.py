@@ -415,3 +415,53 @@ def test_symlinked_shard_outside_the_directory_is_rejected(tmp_path):
     write_config(ck)
     os.symlink(outside / "x.safetensors", ck / "model.safetensors")
     rejected(ck, "safetensors shard escapes checkpoint directory")
+
+
+# ------------------------------------------------ malformed input robustness
+
+from hypothesis import HealthCheck, given, settings  # noqa: E402
+from hypothesis import strategies as st  # noqa: E402
+
+_GOOD_HEADER = json.dumps({
+    "__metadata__": {"format": "mlx"},
+    "model.a.weight": {"dtype": "U32", "shape": [2, 1], "data_offsets": [0, 8]},
+    "model.a.scales": {"dtype": "BF16", "shape": [2, 1], "data_offsets": [8, 12]},
+    "model.a.biases": {"dtype": "BF16", "shape": [2, 1], "data_offsets": [12, 16]},
+}).encode()
+
+
+@settings(max_examples=300, deadline=None, suppress_health_check=[HealthCheck.function_scoped_fixture])
+@given(st.binary(max_size=200), st.integers(0, len(_GOOD_HEADER)), st.integers(0, 40))
+def test_random_and_mutated_headers_fail_cleanly(tmp_path, noise, cut, data_len):
+    """Random bytes spliced into a valid header, truncated headers and data
+    sections of any length: opening either succeeds or raises QmrError, and
+    a checkpoint that opens answers matrix queries the same way."""
+    write_config(tmp_path, quantization={"bits": 4, "group_size": 8})
+    header = _GOOD_HEADER[:cut] + noise + _GOOD_HEADER[cut:]
+    (tmp_path / "model.safetensors").write_bytes(struct.pack("<Q", len(header)) + header + bytes(data_len))
+    try:
+        cp = qmr.Checkpoint(tmp_path)
+    except qmr.QmrError:
+        return
+    with cp:
+        for name in ("model.a", "model.b", "lm_head"):
+            try:
+                cp.matrix(name)
+            except qmr.QmrError:
+                pass
+
+
+@settings(max_examples=200, deadline=None, suppress_health_check=[HealthCheck.function_scoped_fixture])
+@given(st.recursive(st.none() | st.booleans() | st.integers(-2**70, 2**70) | st.floats(allow_nan=False)
+                    | st.text(max_size=8),
+                    lambda inner: st.lists(inner, max_size=4) | st.dictionaries(st.text(max_size=6), inner,
+                                                                                max_size=4),
+                    max_leaves=20))
+def test_arbitrary_json_values_as_headers_fail_cleanly(tmp_path, value):
+    write_config(tmp_path)
+    header = json.dumps(value).encode()
+    (tmp_path / "model.safetensors").write_bytes(struct.pack("<Q", len(header)) + header)
+    try:
+        qmr.Checkpoint(tmp_path).close()
+    except qmr.QmrError:
+        pass
