@@ -96,7 +96,9 @@ def test_config4_wide_block(gpu, batch):
 @pytest.mark.parametrize("rows,cols,batch,meta", [(300, 1024, 100, "bf16"), (128, 512, 64, "f32"),
                                                   (17, 512, 5, "bf16"), (1000, 2048, 256, "f32"),
                                                   (250, 1536, 65, "bf16"), (290, 4096, 40, "f32"),
-                                                  (600, 6400, 33, "bf16"), (17000, 512, 128, "bf16")])
+                                                  (600, 6400, 33, "bf16"), (17000, 512, 128, "bf16"),
+                                                  (300, 1024, 8, "bf16"), (300, 1024, 9, "f32"),
+                                                  (64, 512, 1, "bf16")])
 def test_wide_block_tails_and_metadata(gpu, rows, cols, batch, meta):
     """Wide blocks at ragged row and RHS counts, both wide names, against
     the FP64 oracle. The kernel's K quarters hold 16 groups at cols 4096 and
