@@ -541,7 +541,7 @@ size_t mfma_lds_bytes(uint32_t tps, uint32_t ngm, uint32_t batch, uint32_t rt, b
     return size_t(tps) * (4 * 4 * 2 * batch * 16 + 64) + size_t(rt) * 16 * gp * 4 * (f32_meta ? 2 : 1) + 16;
 }
 
-MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
+MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_ns) {
     MfmaPlan pl;
     if (!affine_mfma_supported(a)) return pl;
     const uint32_t ngm = kTileK / a.group;
@@ -566,6 +566,7 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim) {
     uint32_t best_resident = 1;
     const uint32_t tpe = 8 / a.bits;  // K tiles per 128-byte load entry
     for (uint32_t ns = 1; ns <= tiles && ns <= kMaxSplits; ++ns) {
+        if (force_ns && ns != force_ns) continue;
         uint32_t tps = (tiles + ns - 1) / ns;
         tps = (tps + tpe - 1) / tpe * tpe;  // splits start on an entry
         const uint32_t eff = (tiles + tps - 1) / tps;

@@ -77,7 +77,8 @@ struct MfmaPlan {
     uint32_t rounds = 0;  // rounds of resident workgroups the grid takes
 };
 bool affine_mfma_supported(const AffineArgs &a);
-MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim);
+// force_ns > 0 (tuning hook) keeps only that number of K splits.
+MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_ns = 0);
 // Workspace bytes the plan needs for cross-workgroup partial sums (0 if none).
 size_t affine_mfma_workspace(const MfmaPlan &pl, const AffineArgs &a);
 // `partial` holds affine_mfma_workspace bytes; `counters` holds pl.nbands

@@ -241,7 +241,7 @@ bool rows_preferred(const qmr::MfmaPlan &pl) {
 // shape to the row-owning matrix-core kernel; else the vector-ALU kernels.
 // A forced plan (testing hook) of rr > 0 or rr == -1 selects the vector-ALU
 // tilings, rr == -3 the row-owning matrix-core kernel, rr == -2 the split-K
-// kernel whatever its shape.
+// kernel whatever its shape (with ks > 0 splits, when that count is feasible).
 hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
     const qmr::GemvPlan f = dev->forced_plan;
     if (f.rr == -3 && qmr::affine_rows_supported(a)) {
@@ -249,7 +249,8 @@ hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
         if (pl.rt > 0) return qmr::launch_affine_rows(a, pl, dev->stream);
     }
     if ((f.rr == 0 || f.rr == -2 || f.rr == -3) && qmr::affine_mfma_supported(a)) {
-        const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, dev->limits);
+        const qmr::MfmaPlan pl =
+            qmr::plan_affine_mfma(a, dev->limits, f.rr == -2 && f.ks > 0 ? uint32_t(f.ks) : 0u);
         if (f.rr == 0 && pl.rt > 0 && rows_preferred(pl) && qmr::affine_rows_supported(a)) {
             const qmr::RowsPlan rp = qmr::plan_affine_rows(a, dev->limits);
             if (rp.rt > 0) return qmr::launch_affine_rows(a, rp, dev->stream);
@@ -886,7 +887,8 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
             }
         }
         if ((f.rr == 0 || f.rr == -2 || f.rr == -3) && qmr::affine_mfma_supported(a)) {
-            const qmr::MfmaPlan pl = qmr::plan_affine_mfma(a, device->limits);
+            const qmr::MfmaPlan pl =
+                qmr::plan_affine_mfma(a, device->limits, f.rr == -2 && f.ks > 0 ? uint32_t(f.ks) : 0u);
             if (f.rr == 0 && pl.rt > 0 && rows_preferred(pl) && qmr::affine_rows_supported(a)) {
                 const qmr::RowsPlan rp = qmr::plan_affine_rows(a, device->limits);
                 if (rp.rt > 0) {
