@@ -89,7 +89,11 @@ __device__ __forceinline__ void vmem_order() {
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
 }
 
-template <int BITS, int META, int GROUP, int B, int P, bool PAIRS>
+// FUSE 0: y = W x. FUSE 1: y = r + W x. FUSE 2: the fused MLP form. The
+// fused forms are separate instances so that the plain product's code is
+// untouched by them (runtime tests of their pointers cost the plain GEMV
+// 0.6 us at the metric shape).
+template <int BITS, int META, int GROUP, int B, int P, bool PAIRS, int FUSE>
 __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) {
     constexpr int NGM = kTileK / GROUP;  // quant groups per tile
     constexpr int SLOTS = 16 / NGM;      // A rows per quant group
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     const int r = lane & 15;
     const int lg = lane >> 4;
     const uint32_t RT = uint32_t(nthr) >> 6;
-    const bool mlp = p.w2 != nullptr;
+    constexpr bool mlp = FUSE == 2;
     const uint32_t nmat = mlp ? 2u : 1u;
     const uint32_t mat = mlp ? blockIdx.x / (p.nbands * p.ns) : 0u;
     const uint32_t bid = blockIdx.x - mat * p.nbands * p.ns;
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         if (wave_base + i * nthr >= items) continue;
         const uint32_t it = tid + i * nthr;
         load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), T0 * kTileK + item_col<B>(it), p.cols, it < items);
-        if (mlp) {
+        if constexpr (mlp) {
             const __amdgpu_buffer_rsrc_t nr = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float *>(p.norm), 0, int(p.cols * 4u), kRsrcWord3);
             float nv[8];
@@ -320,8 +324,8 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     if (p.ns == 1 && !mlp) {
         if (writer) {
             const size_t o0 = size_t(t0) * p.rows + row, o1 = o0 + p.rows;
-            if (t0 < B) p.y[o0] = p.r ? p.r[o0] + v0 : v0;
-            if (t0 + 1 < B) p.y[o1] = p.r ? p.r[o1] + v1 : v1;
+            if (t0 < B) p.y[o0] = FUSE == 1 ? p.r[o0] + v0 : v0;
+            if (t0 + 1 < B) p.y[o1] = FUSE == 1 ? p.r[o1] + v1 : v1;
         }
         return;
     }
@@ -350,7 +354,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     float inv[B];
 #pragma unroll
     for (int t = 0; t < B; ++t) inv[t] = 1.f;
-    if (mlp) {
+    if constexpr (mlp) {
         float *sq = reinterpret_cast<float *>(lds);
 #pragma unroll
         for (int t = 0; t < B; ++t) {
@@ -389,7 +393,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
 #pragma unroll
         for (uint32_t k = 1; k < kMaxSplits; ++k) v += pv[k];
         const size_t o = size_t(t) * p.rows + rr;
-        if (mlp) {
+        if constexpr (mlp) {
             // The up matrix's partials follow the gate's ns blocks.
             const float *pu = p.partial + size_t(p.ns) * stride + size_t(t) * p.rows + rr;
 #pragma unroll
@@ -406,7 +410,7 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
             const float g = v * it;
             p.y[o] = g * (1.0f / (1.0f + expf(-g))) * (u * it);
         } else {
-            p.y[o] = p.r ? p.r[o] + v : v;
+            p.y[o] = FUSE == 1 ? p.r[o] + v : v;
         }
     }
     if (tid == 0) __hip_atomic_store(&p.counters[band], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -416,13 +420,16 @@ constexpr int kRing = 2;  // entries in flight per wave
 
 template <int BITS, int META, int GROUP, int B, bool PAIRS>
 hipError_t launch_b(const MfmaParams &p, uint32_t rt, size_t lds, hipStream_t stream) {
-    auto kernel = affine_mfma_kernel<BITS, META, GROUP, B, kRing, PAIRS>;
-    static size_t configured = 0;
-    if (lds > 65536 && lds > configured) {
+    const int fuse = p.w2 ? 2 : p.r ? 1 : 0;
+    auto kernel = fuse == 2   ? affine_mfma_kernel<BITS, META, GROUP, B, kRing, PAIRS, 2>
+                  : fuse == 1 ? affine_mfma_kernel<BITS, META, GROUP, B, kRing, PAIRS, 1>
+                              : affine_mfma_kernel<BITS, META, GROUP, B, kRing, PAIRS, 0>;
+    static size_t configured[3] = {0, 0, 0};
+    if (lds > 65536 && lds > configured[fuse]) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         if (e != hipSuccess) return e;
-        configured = lds;
+        configured[fuse] = lds;
     }
     hipLaunchKernelGGL(kernel, dim3(p.nbands * p.ns * (p.w2 ? 2u : 1u)), dim3(rt * 64), lds, stream, p);
     return hipGetLastError();
@@ -465,16 +472,17 @@ hipError_t launch_meta(const MfmaParams &p, uint32_t group, uint32_t batch, bool
     }
 }
 
-// The kernel instance for a format, for occupancy queries.
+// The kernel instance for a format, for occupancy queries (the plain form's;
+// the fused forms plan with its occupancy).
 template <int BITS, int META, int GROUP>
 const void *instance_group(uint32_t batch, bool pairs) {
     constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
     auto pick = [&](auto bconst) -> const void * {
         constexpr int B = decltype(bconst)::value;
         if constexpr (META != 0) {
-            if (pairs) return reinterpret_cast<const void *>(affine_mfma_kernel<BITS, META, GROUP, B, kRing, true>);
+            if (pairs) return reinterpret_cast<const void *>(affine_mfma_kernel<BITS, META, GROUP, B, kRing, true, 0>);
         }
-        return reinterpret_cast<const void *>(affine_mfma_kernel<BITS, META, GROUP, B, kRing, false>);
+        return reinterpret_cast<const void *>(affine_mfma_kernel<BITS, META, GROUP, B, kRing, false, 0>);
     };
     switch (batch) {
         case 1: return pick(std::integral_constant<int, 1>{});
