@@ -165,6 +165,18 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *     w, s, b, x, y; params rows, cols, bits, group, batch with
  *     1 <= batch <= 256; x [batch][cols], y [batch][rows] token-major;
  *     threads = rows*32. Q4/g64 runs on MFMA; meant for chunked prefill.
+ *     Batches of up to eight run as successive blocks of up to four.
+ *   "matmul_affine_add" / "_bf16" / "_f16meta"
+ *     y = r + W x, the down projection with the decoder's residual add
+ *     (src/engine.rs:763-765). Buffers w, s, b, x, r, y; params as the
+ *     blocks (batch 1..4); r and y [batch][rows]; y may be exactly r's view
+ *     (in place), any other overlap is rejected. Matrix-core formats only.
+ *   "mlp_gate_up_swiglu" / "_bf16" / "_f16meta"
+ *     y = silu(G n) * (U n), n = rms_norm(x, norm, eps): the decoder MLP's
+ *     rms_norm + gate + up + swiglu (src/engine.rs:748-762) in one launch.
+ *     Buffers gate w/s/b, up w/s/b (same shape and format), x [batch][cols],
+ *     norm [cols], y [batch][rows]; params rows, cols, bits, group, batch
+ *     (1..4), eps as FP32 bits (finite, positive). Matrix-core formats only.
  *   "matvec_affine_f16meta", "matmul_affine_f16meta", "embed_affine_f16meta"
  *     As the FP32-metadata names, with scales/biases stored as IEEE binary16
  *     (the dtype MLX checkpoints ship). The reference expands F16 metadata
@@ -173,12 +185,15 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  */
 
 /* ---- Testing and tuning hooks (no counterpart in the reference). ---- */
-/* Force the GEMV kernel and tiling; 0,0 = planner (split-K matrix-core
- * kernel where supported, else the vector-ALU kernels).
- *   rr = -3: row-owning matrix-core kernel (opt-in); ks = j*10000 + rt*100 + kw
- *            pins its workgroup shape (rt row tiles x kw K waves) and, when
- *            j > 0, the entries per wave per staged chunk; 0 = its planner.
- *   rr = -2: split-K matrix-core kernel (ks ignored).
+/* Force the GEMV kernel and tiling; 0,0 = planner (the split-K matrix-core
+ * kernel where supported, the row-owning one past one round of resident
+ * workgroups or for splits under four K tiles, else the vector-ALU kernels).
+ *   rr = -3: row-owning matrix-core kernel (also the MLP form's); ks =
+ *            j*10000 + rt*100 + kw pins its workgroup shape (rt row tiles x
+ *            kw K waves) and, when j > 0, the entries per wave per staged
+ *            chunk; 0 = its planner.
+ *   rr = -2: split-K matrix-core kernel; ks > 0 keeps only that number of
+ *            K splits when it is feasible, 0 = its planner.
  *   rr = -1: the vector-ALU streaming single-RHS kernel (blocks then use
  *            the row-slot tiling).
  *   rr > 0 with ks > 0: the vector-ALU row-slot kernel with `rr` rows per
