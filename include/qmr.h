@@ -168,12 +168,12 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *     Batches of up to eight run as successive blocks of up to four.
  *   "matmul_affine_add" / "_bf16" / "_f16meta"
  *     y = r + W x, the down projection with the decoder's residual add
- *     (src/engine.rs:763-765). Buffers w, s, b, x, r, y; params as the
+ *     (src/engine.rs:764-765). Buffers w, s, b, x, r, y; params as the
  *     blocks (batch 1..4); r and y [batch][rows]; y may be exactly r's view
  *     (in place), any other overlap is rejected. Matrix-core formats only.
  *   "mlp_gate_up_swiglu" / "_bf16" / "_f16meta"
  *     y = silu(G n) * (U n), n = rms_norm(x, norm, eps): the decoder MLP's
- *     rms_norm + gate + up + swiglu (src/engine.rs:748-762) in one launch.
+ *     rms_norm + gate + up + swiglu (src/engine.rs:748-763) in one launch.
  *     Buffers gate w/s/b, up w/s/b (same shape and format), x [batch][cols],
  *     norm [cols], y [batch][rows]; params rows, cols, bits, group, batch
  *     (1..4), eps as FP32 bits (finite, positive). Matrix-core formats only.
