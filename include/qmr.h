@@ -193,7 +193,8 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *            kw K waves) and, when j > 0, the entries per wave per staged
  *            chunk; 0 = its planner.
  *   rr = -2: split-K matrix-core kernel; ks > 0 keeps only that number of
- *            K splits when it is feasible, 0 = its planner.
+ *            K splits when it is feasible (else the planner's count), 0 =
+ *            its planner.
  *   rr = -1: the vector-ALU streaming single-RHS kernel (blocks then use
  *            the row-slot tiling).
  *   rr > 0 with ks > 0: the vector-ALU row-slot kernel with `rr` rows per

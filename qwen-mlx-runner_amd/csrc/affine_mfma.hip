@@ -600,6 +600,7 @@ MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim, uint32_t
         }
     }
     if (pl.ns == 0) {
+        if (force_ns) return plan_affine_mfma(a, lim, 0);  // infeasible forced count: the planner's
         pl.rt = 0;
         return pl;
     }

@@ -298,3 +298,20 @@ def test_dense_f16_products_at_scale(gpu, rows, cols, batch):
     assert got[-1] == 7.0, "wrote past y"
     want = oracle.dense_f16_f64(w16, x, rows, cols, batch)
     assert_gate(got[:-1], want, f"dense {rows}x{cols} B{batch}")
+
+
+def test_forced_split_count_is_honoured_and_correct(gpu):
+    """The tuning hook rr = -2, ks = n keeps only n K splits when feasible
+    (17408x5120 at B=1: 10 splits), and the product still meets the gate;
+    an infeasible count falls back to the planner's."""
+    rows, cols = synth.MLP_SHAPES["gate_up"]
+    default = gpu.gemv_plan(rows, cols, 4, 1)
+    gpu.set_gemv_plan(-2, 10)
+    try:
+        assert gpu.gemv_plan(rows, cols, 4, 1) == (-2, 10)
+        got, want = _launch_three(gpu, rows, cols, 1, 41)
+        assert_gate(got[0], want, "forced 10 splits")
+        gpu.set_gemv_plan(-2, 31)
+        assert gpu.gemv_plan(rows, cols, 4, 1) == default
+    finally:
+        gpu.set_gemv_plan(0, 0)
