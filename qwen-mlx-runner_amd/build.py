@@ -31,6 +31,7 @@ SOURCES = [
     ("affine_gemv.hip", ["-x", "hip"]),
     ("affine_mfma.hip", ["-x", "hip"]),
     ("affine_rows.hip", ["-x", "hip"]),
+    ("affine_tile.hip", ["-x", "hip"]),
     ("misc_kernels.hip", ["-x", "hip"]),
     # MFMA accumulators in VGPRs: the wide kernel's FP32 epilogue adds into
     # the same registers its bias MFMAs accumulate into.

@@ -1,0 +1,597 @@
+// Streaming dequantise + GEMV / small block (batch 1..4) over MLX affine
+// packed weights on the gfx950 matrix cores: row bands of 16-row tiles, each
+// band's K range cut into at most a few long splits across workgroups and
+// into contiguous per-wave ranges inside a workgroup.
+//
+// Same product and numerics as affine_mfma.hip (operands, code encoding and
+// the tile product are in mfma_common.hpp):
+//     y[t*rows + r] = sum_g ( s[r,g] * sum_{c in g} q[r,c] * x[t,c]
+//                           + b[r,g] * sum_{c in g} x[t,c] )
+// which is the reference's per-weight affine dot (kernels/qwen.metal:40-68,
+// kernels/matmul_block.metal:20-79) in the factored form of
+// kernels/matvec_fast.metal:11-15.
+//
+// Decomposition. Workgroup (band, split) owns TR 16-row tiles over the
+// split's K range and runs KW waves per tile; wave (tile, kw) streams the
+// contiguous run kw of the split's 128-byte entries for its 16 rows. Grid =
+// nbands x ns, blockIdx = band + nbands * split.
+//
+// Why this shape (measured on MI355X with pure-read kernels of the same
+// bytes, back-to-back launches over rotating copies):
+//   - The order of a tile's loads costs little (16-byte loads in MFMA lane
+//     order read ~14% slower than eight lanes per 128-byte line).
+//   - x is read from L2 by every workgroup that needs it, and that traffic
+//     competes with the weight stream: one 16-byte x load per lane per entry
+//     interleaved with the stream added ~20% at 5120x17408 for 16-row
+//     workgroups. So x is staged once per workgroup, up front, shared by all
+//     TR*16 rows, and converted there into MFMA operand images in LDS.
+//   - A CU streams at most ~45 GB/s here, so a grid needs more than ~160
+//     busy CUs: tall bands are cut into a few K splits rather than made
+//     into fewer workgroups.
+//   - Metadata read as the 32-byte pieces of short splits cost ~20%; long
+//     splits read each row's metadata as one run, staged in LDS up front.
+// End of a band. The KW partial sums of a row are added in LDS in wave order.
+// With ns > 1 splits, splits 0..ns-2 publish their sums as 64-bit slots
+// {value, launch epoch} and the band's last split (the highest workgroup
+// index, dispatched last) reads them; a slot whose epoch is the current
+// launch's is complete, so one read both checks and fetches it, with no
+// counter and no fence chain. The sum is taken in split order, so results
+// do not depend on timing. The wait is bounded: past the host's spin limit
+// the workgroup writes NaN and exits, so every wave always finishes.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <type_traits>
+
+#include "kernels.hpp"
+#include "mfma_common.hpp"
+
+namespace qmr {
+namespace {
+
+using namespace mfma;
+
+constexpr int kMaxThreads = 512;  // up to 8 waves: x staging needs up to 8 items of registers per thread
+constexpr int kMetaUnits = 4;  // 16-byte metadata loads per thread and plane (fast path)
+
+struct BandParams {
+    const uint32_t *w;
+    const void *s;
+    const void *b;
+    const float *x;
+    float *y;
+    const float *r;              // residual added in the final store (may alias y), or null
+    unsigned long long *partial;  // [ns-1][B][rows] {value, epoch} slots (ns > 1)
+    uint32_t epoch;
+    uint32_t spin_limit;
+    uint32_t rows, cols;
+    uint32_t w_bytes, m_bytes;  // extents of the code and metadata views
+    uint32_t tr, kw, ns, nbands;
+    uint32_t n_entries;   // 128-byte code entries per row (the last may be partial)
+    uint32_t tiles;       // 128-column K tiles
+    uint32_t align_e;     // split boundaries are multiples of this many entries
+    uint32_t gp;          // LDS pitch of a row's staged metadata (odd)
+    uint32_t meta_bytes;  // LDS bytes of the staged metadata (16-byte multiple)
+    uint32_t img_bytes;   // LDS bytes of the staged x images
+};
+
+// First entry of split s (aligned; the last split ends at n_entries).
+__device__ __forceinline__ uint32_t split_begin(uint32_t s, uint32_t ns, uint32_t n_entries, uint32_t align) {
+    if (s >= ns) return n_entries;
+    const uint32_t raw = uint32_t((uint64_t(s) * n_entries) / ns);
+    const uint32_t a = (raw + align / 2) / align * align;
+    return a < n_entries ? a : n_entries;
+}
+
+template <int BITS, int GROUP, int B>
+constexpr uint32_t tile_img_bytes() {
+    constexpr int NGM = kTileK / GROUP;
+    constexpr int HALF = 16 / NGM / 2;
+    return 4u * 4 * 2 * B * 16 + uint32_t(NGM) * (HALF / 2) * 16;
+}
+
+// XI: x items (8 columns each) staged per thread.
+template <int BITS, int META, int GROUP, int B, int XI, int P, bool RESID>
+__global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) {
+    constexpr int NGM = kTileK / GROUP;  // quant groups per tile
+    constexpr int SLOTS = 16 / NGM;      // A rows per quant group
+    constexpr int HALF = SLOTS / 2;      // RHS per quant group in D (>= B)
+    constexpr int NLD = BITS / 4;        // 16-byte code pieces per lane per tile
+    constexpr int TPE = 8 / BITS;        // K tiles per 128-byte entry
+    constexpr int MB = META == 0 ? 4 : 2;
+    constexpr int VEC = 16 / MB;  // metadata values per 16-byte load
+    constexpr uint32_t TIMG = tile_img_bytes<BITS, GROUP, B>();
+    constexpr uint32_t TIMG_A = 4u * 4 * 2 * B * 16;
+    static_assert(2 * B <= SLOTS, "batch does not fit the slot layout");
+
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int tid = threadIdx.x;
+    const int nthr = blockDim.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int r = lane & 15;
+    const int lg = lane >> 4;
+    const uint32_t KW = p.kw;
+    const uint32_t ti = uint32_t(wave) / KW;
+    const uint32_t kw = uint32_t(wave) - ti * KW;
+    const uint32_t band = blockIdx.x % p.nbands;
+    const uint32_t split = blockIdx.x / p.nbands;
+    const uint32_t band_row0 = band * p.tr * 16u;
+    const uint32_t tile_row0 = band_row0 + ti * 16u;
+    const uint32_t nG = p.cols / GROUP;
+    const uint32_t Gp = p.gp;
+    // The split's entries, tiles, groups and columns.
+    const uint32_t SE0 = split_begin(split, p.ns, p.n_entries, p.align_e);
+    const uint32_t SE1 = split_begin(split + 1, p.ns, p.n_entries, p.align_e);
+    const uint32_t ST0 = SE0 * TPE;
+    const uint32_t ST1 = min(SE1 * TPE, p.tiles);
+    const uint32_t nT = ST1 - ST0;
+    const uint32_t G0 = ST0 * NGM;
+    const uint32_t G1 = min(ST1 * NGM, nG);
+    // This wave's entries.
+    const uint32_t nSE = SE1 - SE0;
+    const uint32_t E0 = SE0 + kw * nSE / KW;
+    const uint32_t E1 = SE0 + (kw + 1) * nSE / KW;
+
+    uint32_t *ldsM = reinterpret_cast<uint32_t *>(lds);  // [tr*16][Gp] s|b<<16, or [tr*16][Gp][2] f32
+    unsigned char *img = lds + p.meta_bytes;              // [nT] tile images
+    float *red = reinterpret_cast<float *>(lds + p.meta_bytes + p.img_bytes);
+
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(p.w), 0, int(p.w_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t sr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.s), 0, int(p.m_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t br =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.b), 0, int(p.m_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(p.x), 0, int(uint32_t(B) * p.cols * 4u), kRsrcWord3);
+
+    // ---- 1. The split's x, requested first: at the start every workgroup
+    // queues its loads behind those of the workgroups dispatched before it on
+    // its CU, and nothing can be multiplied before x is staged. Item it = ((Tl*B + t)*4 + g)*4 + m covers the 8
+    // columns (ST0 + Tl)*128 + 32g + 8m of RHS t (mfma_common.hpp). ----
+    const uint32_t items = nT * B * 16u;
+    float xv[XI][8];
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
+        load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), ST0 * kTileK + item_col<B>(it), p.cols, it < items);
+    }
+
+    // ---- 2. Metadata of the band's rows over the split's groups: one run
+    // per row and plane, as 16-byte loads when the runs are 16-byte aligned
+    // (every checkpoint shape with aligned splits). Rows past the matrix read
+    // zeros through the buffer range check. ----
+    const uint32_t run_bytes = (G1 - G0) * MB;
+    const bool vec_meta = (nG * MB) % 16 == 0 && (G0 * MB) % 16 == 0 && run_bytes % 16 == 0;
+    const uint32_t upr = vec_meta ? run_bytes / 16 : 0u;  // units per row
+    const uint32_t units = p.tr * 16u * upr;
+    auto unit_off = [&](uint32_t f) -> uint32_t {
+        const uint32_t rl = f / upr;
+        return ((band_row0 + rl) * nG + G0) * MB + (f - rl * upr) * 16u;
+    };
+    u4 ms[kMetaUnits], mbv[kMetaUnits];
+#pragma unroll
+    for (int u = 0; u < kMetaUnits; ++u) {
+        const uint32_t f = uint32_t(tid) + uint32_t(u * nthr);
+        const uint32_t off = f < units ? unit_off(f) : kOut;
+        ms[u] = __builtin_amdgcn_raw_buffer_load_b128(sr, int(off), 0, 0);
+        mbv[u] = __builtin_amdgcn_raw_buffer_load_b128(br, int(off), 0, 0);
+    }
+
+    // ---- 3. The first P entries of codes. An entry is 128 contiguous bytes
+    // of each of the tile's 16 rows, read with two 16-byte loads per lane:
+    // rows 0-7 then 8-15, eight lanes per row; lanes r and r^8 swap one
+    // piece through DPP after the loads land. ----
+    const bool lo_half = r < 8;
+    const uint32_t kp = BITS == 4 ? uint32_t(lg) : 2u * lg;          // 16-byte piece kept
+    const uint32_t sp = BITS == 4 ? uint32_t(lg) + 4 : 2u * lg + 1;  // piece sent to lane r^8
+    const uint32_t piece1 = lo_half ? kp : sp;
+    const uint32_t piece2 = lo_half ? sp : kp;
+    const uint32_t row_bytes = p.cols / 32 * (BITS * 4);
+    const uint32_t rowA = tile_row0 + (r & 7), rowB = tile_row0 + 8 + (r & 7);
+    const uint32_t base1 = rowA * row_bytes + 16 * piece1;
+    const uint32_t base2 = rowB * row_bytes + 16 * piece2;
+    const bool okA = rowA < p.rows, okB = rowB < p.rows;
+    auto issue = [&](u4 (&c)[2], uint32_t E) {
+        const uint32_t eb = E * 128;
+        const uint32_t o1 = (E < E1 && okA && eb + 16 * piece1 < row_bytes) ? base1 + eb : kOut;
+        const uint32_t o2 = (E < E1 && okB && eb + 16 * piece2 < row_bytes) ? base2 + eb : kOut;
+        c[0] = __builtin_amdgcn_raw_buffer_load_b128(wr, int(o1), 0, kAuxStream);
+        c[1] = __builtin_amdgcn_raw_buffer_load_b128(wr, int(o2), 0, kAuxStream);
+    };
+    u4 ring[P][2];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        issue(ring[j], E0 + j);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- 4. Metadata to LDS. ----
+    if (vec_meta) {
+        auto put = [&](uint32_t f, const u4 &sv, const u4 &bv) {
+            const uint32_t rl = f / upr;
+            const uint32_t g = (f - rl * upr) * VEC;
+            if constexpr (META == 0) {
+                uint32_t *dst = ldsM + (rl * Gp + g) * 2;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dst[2 * e] = sv[e];
+                    dst[2 * e + 1] = bv[e];
+                }
+            } else {
+                uint32_t *dst = ldsM + rl * Gp + g;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dst[2 * e] = __builtin_amdgcn_perm(bv[e], sv[e], 0x05040100u);
+                    dst[2 * e + 1] = __builtin_amdgcn_perm(bv[e], sv[e], 0x07060302u);
+                }
+            }
+        };
+#pragma unroll
+        for (int u = 0; u < kMetaUnits; ++u) {
+            const uint32_t f = uint32_t(tid) + uint32_t(u * nthr);
+            if (f < units) put(f, ms[u], mbv[u]);
+        }
+        // Workgroups with more runs than the unrolled loads read the rest here.
+        for (uint32_t f = uint32_t(tid) + uint32_t(kMetaUnits * nthr); f < units; f += uint32_t(nthr)) {
+            const uint32_t off = unit_off(f);
+            put(f, __builtin_amdgcn_raw_buffer_load_b128(sr, int(off), 0, 0),
+                __builtin_amdgcn_raw_buffer_load_b128(br, int(off), 0, 0));
+        }
+    } else {
+        const uint32_t ng = G1 - G0;
+        for (uint32_t f = uint32_t(tid); f < p.tr * 16u * ng; f += uint32_t(nthr)) {
+            const uint32_t rl = f / ng;
+            const uint32_t g = f - rl * ng;
+            const uint32_t off = ((band_row0 + rl) * nG + G0 + g) * MB;
+            if constexpr (META == 0) {
+                ldsM[(rl * Gp + g) * 2] = __builtin_amdgcn_raw_buffer_load_b32(sr, int(off), 0, 0);
+                ldsM[(rl * Gp + g) * 2 + 1] = __builtin_amdgcn_raw_buffer_load_b32(br, int(off), 0, 0);
+            } else {
+                const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(sr, int(off), 0, 0);
+                const uint32_t bv = __builtin_amdgcn_raw_buffer_load_b16(br, int(off), 0, 0);
+                ldsM[rl * Gp + g] = (sv & 0xFFFFu) | (bv << 16);
+            }
+        }
+    }
+    // Groups of a partial last K tile past the matrix: zero entries (their
+    // products are zero, and finite metadata keeps them so).
+    {
+        const uint32_t extra = nT * NGM - (G1 - G0);
+        for (uint32_t f = uint32_t(tid); f < p.tr * 16u * extra; f += uint32_t(nthr)) {
+            const uint32_t rl = f / extra;
+            const uint32_t g = (G1 - G0) + (f - rl * extra);
+            if constexpr (META == 0) {
+                ldsM[(rl * Gp + g) * 2] = 0u;
+                ldsM[(rl * Gp + g) * 2 + 1] = 0u;
+            } else {
+                ldsM[rl * Gp + g] = 0u;
+            }
+        }
+    }
+
+    // ---- 5. x as MFMA operand images (hi/lo f16, group sums, epilogue
+    // factors), tile by tile; zero sums and factors of absent RHS. ----
+    u4 *imgA = reinterpret_cast<u4 *>(img);
+    float4 *imgS = reinterpret_cast<float4 *>(img + nT * TIMG_A);
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
+        if (i > 0 && uint32_t(tid) - uint32_t(lane) + uint32_t(i * nthr) >= items) break;  // whole waves in or out
+        stage_x_item<BITS, GROUP, B>(xv[i], it, it < items, lane, imgA, imgS);
+    }
+    stage_x_pads<GROUP, B>(nT, tid, nthr, imgS);
+    lds_barrier();
+
+    // ---- 6. Stream the wave's entries. ----
+    const LaneMap<GROUP, B> L(lane);
+    const int t0 = L.t0;
+    const uint32_t m_row = (ti * 16u + uint32_t(r)) * Gp + uint32_t(L.gD);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    h8 a[4] = {h8{}, h8{}, h8{}, h8{}};
+    auto compute = [&](const u4 (&c)[NLD], uint32_t Tl) {
+        float sv, bv;
+        meta_entry<META>(ldsM + (m_row + Tl * NGM) * (META == 0 ? 2 : 1), sv, bv);
+        const float4 sx = imgS[(Tl * NGM + L.gD) * (HALF / 2) + t0 / 2];
+        tile_product<BITS, META, GROUP, B>(c, L, imgA + Tl * 4 * (8 * B), sv, bv, sx, a, acc);
+    };
+    auto exchange = [&](const u4 (&c)[2], u4 &kept, u4 &got) {
+        u4 send;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            kept[d] = lo_half ? c[0][d] : c[1][d];
+            send[d] = lo_half ? c[1][d] : c[0][d];
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) got[d] = uint32_t(__builtin_amdgcn_mov_dpp(int(send[d]), 0x128, 0xF, 0xF, false));
+    };
+    const uint32_t nE = E1 - E0;
+    for (uint32_t base = 0; base < nE; base += P) {
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            const uint32_t i = base + j;
+            if (i < nE) {
+                const uint32_t E = E0 + i;
+                u4 kept, got;
+                exchange(ring[j], kept, got);
+                const uint32_t Tl = E * TPE - ST0;
+                if constexpr (BITS == 4) {
+                    const u4 c0[1] = {kept};
+                    compute(c0, Tl);
+                    if (E * 2 + 1 < p.tiles) {
+                        const u4 c1[1] = {got};
+                        compute(c1, Tl + 1);
+                    }
+                } else {
+                    const u4 c[2] = {kept, got};
+                    compute(c, Tl);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            issue(ring[j], E0 + i + P);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // ---- 7. Combine hi/lo slots and quant groups, add the KW partial sums
+    // of each row in wave order, then finish the band across splits. ----
+    float v0, v1;
+    combine_slots<GROUP>(acc, v0, v1);
+    constexpr int WRITERS = 4 / NGM;  // lane groups holding distinct RHS pairs
+    if (lg < WRITERS) {
+        float *dst = red + (size_t(wave) * B) * 16u + uint32_t(r);
+        if (t0 < B) dst[size_t(t0) * 16u] = v0;
+        if (t0 + 1 < B) dst[size_t(t0 + 1) * 16u] = v1;
+    }
+    __syncthreads();
+    const uint32_t outs = p.tr * 16u * B;
+    if (uint32_t(tid) >= outs) return;
+    const uint32_t tt = uint32_t(tid) / (16u * B);  // tile within the band
+    const uint32_t t = (uint32_t(tid) / 16u) % B;
+    const uint32_t rr = uint32_t(tid) % 16u;
+    const uint32_t row = band_row0 + tt * 16u + rr;
+    if (row >= p.rows) return;
+    const float *src = red + (size_t(tt * KW) * B + t) * 16u + rr;
+    float v = src[0];
+    for (uint32_t k = 1; k < KW; ++k) v += src[size_t(k) * B * 16u];
+    const size_t oy = size_t(t) * p.rows + row;
+    if (p.ns > 1) {
+        const size_t slot = oy;  // [split][B][rows]
+        const size_t stride = size_t(B) * p.rows;
+        if (split + 1 < p.ns) {
+            const unsigned long long word = (static_cast<unsigned long long>(p.epoch) << 32) | __float_as_uint(v);
+            __hip_atomic_store(p.partial + size_t(split) * stride + slot, word, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        // The band's last split: the other splits' sums, in split order.
+        float sum = 0.f;
+        bool ok = true;
+        for (uint32_t k = 0; k + 1 < p.ns; ++k) {
+            unsigned long long *q = p.partial + size_t(k) * stride + slot;
+            unsigned long long word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (uint32_t spin = 0; uint32_t(word >> 32) != p.epoch; ++spin) {
+                if (spin >= p.spin_limit) {
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+                word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            const float pv = __uint_as_float(uint32_t(word));
+            sum = k == 0 ? pv : sum + pv;
+        }
+        v = ok ? sum + v : __builtin_nanf("");
+    }
+    p.y[oy] = RESID ? p.r[oy] + v : v;
+}
+
+template <int BITS, int META, int GROUP, int B, int XI, int P, bool RESID>
+hipError_t launch_inst(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
+    auto kernel = affine_band_kernel<BITS, META, GROUP, B, XI, P, RESID>;
+    static size_t configured = 0;
+    if (pl.lds > 65536 && pl.lds > configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(pl.lds));
+        if (e != hipSuccess) return e;
+        configured = pl.lds;
+    }
+    hipLaunchKernelGGL(kernel, dim3(pl.nbands * pl.ns), dim3(pl.tr * pl.kw * 64), pl.lds, stream, p);
+    return hipGetLastError();
+}
+
+template <int BITS, int META, int GROUP, int B, int XI>
+hipError_t launch_xi(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
+    const bool resid = p.r != nullptr;
+    if (pl.ring >= 4)
+        return resid ? launch_inst<BITS, META, GROUP, B, XI, 4, true>(p, pl, stream)
+                     : launch_inst<BITS, META, GROUP, B, XI, 4, false>(p, pl, stream);
+    return resid ? launch_inst<BITS, META, GROUP, B, XI, 2, true>(p, pl, stream)
+                 : launch_inst<BITS, META, GROUP, B, XI, 2, false>(p, pl, stream);
+}
+
+template <int BITS, int META, int GROUP, int B>
+hipError_t launch_b(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
+    if (pl.xi <= 4) return launch_xi<BITS, META, GROUP, B, 4>(p, pl, stream);
+    return launch_xi<BITS, META, GROUP, B, 8>(p, pl, stream);
+}
+
+template <int BITS, int META, int GROUP>
+hipError_t launch_group(const BandParams &p, const TilePlan &pl, uint32_t batch, hipStream_t stream) {
+    constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
+    switch (batch) {
+        case 1: return launch_b<BITS, META, GROUP, 1>(p, pl, stream);
+        case 2: return launch_b<BITS, META, GROUP, 2>(p, pl, stream);
+        case 3:
+            if constexpr (MAXB >= 3) return launch_b<BITS, META, GROUP, 3>(p, pl, stream);
+            break;
+        case 4:
+            if constexpr (MAXB >= 4) return launch_b<BITS, META, GROUP, 4>(p, pl, stream);
+            break;
+        default: break;
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int BITS, int META>
+hipError_t launch_meta(const BandParams &p, const TilePlan &pl, uint32_t group, uint32_t batch,
+                       hipStream_t stream) {
+    switch (group) {
+        case 32: return launch_group<BITS, META, 32>(p, pl, batch, stream);
+        case 64: return launch_group<BITS, META, 64>(p, pl, batch, stream);
+        case 128: return launch_group<BITS, META, 128>(p, pl, batch, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+uint32_t host_split_begin(uint32_t s, uint32_t ns, uint32_t n_entries, uint32_t align) {
+    if (s >= ns) return n_entries;
+    const uint32_t raw = uint32_t((uint64_t(s) * n_entries) / ns);
+    const uint32_t a = (raw + align / 2) / align * align;
+    return a < n_entries ? a : n_entries;
+}
+
+}  // namespace
+
+bool affine_tile_supported(const AffineArgs &a) {
+    if (a.up_w) return false;
+    if (a.bits != 4 && a.bits != 8) return false;
+    if (a.group != 32 && a.group != 64 && a.group != 128) return false;
+    const uint32_t maxb = (16 / (kTileK / a.group)) / 2;
+    if (a.batch < 1 || a.batch > maxb) return false;
+    if (a.cols == 0 || a.rows == 0 || a.cols % 32 != 0 || a.cols % a.group != 0) return false;
+    if ((reinterpret_cast<uintptr_t>(a.w) & 15) != 0) return false;
+    const uint64_t w_bytes = uint64_t(a.rows) * a.cols * a.bits / 8;
+    const uint64_t m_bytes = uint64_t(a.rows) * (a.cols / a.group) * (a.meta == Meta::F32 ? 4 : 2);
+    return w_bytes < (1ull << 31) && m_bytes < (1ull << 31) && uint64_t(a.batch) * a.cols * 4 < (1ull << 31);
+}
+
+TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_kw, uint32_t force_tr,
+                          uint32_t force_ns, uint32_t force_ring) {
+    TilePlan pl;
+    if (!affine_tile_supported(a)) return pl;
+    const uint32_t row_tiles = (a.rows + 15) / 16;
+    const uint32_t row_bytes = a.cols / 32 * (a.bits * 4);
+    const uint32_t n_entries = (row_bytes + 127) / 128;
+    const uint32_t ngm = kTileK / a.group;
+    const uint32_t tpe = 8 / a.bits;
+    const uint32_t tiles = (a.cols + kTileK - 1) / kTileK;
+    const uint32_t mb = a.meta == Meta::F32 ? 4 : 2;
+    const uint32_t align_e = std::max(1u, 16u / (mb * tpe * ngm));
+    const uint32_t cus = lim.num_cus > 0 ? uint32_t(lim.num_cus) : 256u;
+    const size_t timg = size_t(4) * 4 * 2 * a.batch * 16 + size_t(ngm) * ((16 / ngm / 2) / 2) * 16;
+    // Candidate shapes: tr tiles per band, ns K splits, kw waves per tile.
+    // Score (fitted to the read-pattern measurements): workgroups near one
+    // per CU or more but no more than resident, about 1.5-2 waves per SIMD,
+    // rows per band as many as that allows (x traffic), few splits.
+    double best = 1e30;
+    for (uint32_t tr : {1u, 2u, 4u, 8u}) {
+        if (force_tr && tr != force_tr) continue;
+        if (tr > row_tiles && tr > 1) continue;
+        const uint32_t nbands = (row_tiles + tr - 1) / tr;
+        for (uint32_t ns : {1u, 2u, 3u, 4u}) {
+            if (force_ns && ns != force_ns) continue;
+            if (ns * align_e > n_entries) continue;
+            // The largest split (entries) after alignment.
+            uint32_t max_se = 0;
+            for (uint32_t s = 0; s < ns; ++s) {
+                const uint32_t e0 = host_split_begin(s, ns, n_entries, align_e);
+                const uint32_t e1 = host_split_begin(s + 1, ns, n_entries, align_e);
+                if (e1 <= e0) max_se = 0x7FFFFFFF;
+                else max_se = std::max(max_se, e1 - e0);
+            }
+            if (max_se == 0x7FFFFFFF) continue;
+            const uint32_t max_tiles = std::min(max_se * tpe, tiles);
+            for (uint32_t kw : {1u, 2u, 4u, 8u}) {
+                if (force_kw && kw != force_kw) continue;
+                const uint32_t threads = tr * kw * 64;
+                if (threads > uint32_t(kMaxThreads) || kw > max_se) continue;
+                const uint32_t items = max_tiles * a.batch * 16;
+                const uint32_t xi = (items + threads - 1) / threads;
+                if (xi > 8) continue;
+                const uint32_t gp = (max_tiles * ngm) | 1u;
+                const size_t meta = (size_t(tr) * 16 * gp * 4 * (a.meta == Meta::F32 ? 2 : 1) + 15) & ~size_t(15);
+                const size_t img = size_t(max_tiles) * timg;
+                const size_t lds = meta + img + size_t(tr * kw) * a.batch * 16 * 4;
+                if (lds > lim.max_lds_per_block) continue;
+                const double wgs = double(nbands) * ns;
+                const double waves = wgs * tr * kw;
+                // Workgroups per CU rounded up, against the even share.
+                const double per_cu = std::ceil(wgs / cus) / (wgs / cus);
+                double score = std::fabs(std::log(waves / (1.5 * 4 * cus)));
+                if (wgs < 0.6 * cus) score += 2.0 * std::log(0.6 * cus / wgs);
+                score += 0.5 * std::log(per_cu);
+                score += 0.15 * (ns - 1);
+                // x read from L2 once per band, relative to the weight bytes.
+                const double wbytes = double(a.rows) * row_bytes + 2.0 * a.rows * (a.cols / a.group) * mb;
+                score += 2.0 * double(nbands) * a.batch * a.cols * 4.0 / wbytes;
+                if (score < best - 1e-9 || (force_kw && force_tr && force_ns)) {
+                    best = score;
+                    pl.kw = kw;
+                    pl.tr = tr;
+                    pl.ns = ns;
+                    pl.nbands = nbands;
+                    pl.n_entries = n_entries;
+                    pl.tiles = tiles;
+                    pl.align_e = align_e;
+                    pl.gp = gp;
+                    pl.meta_bytes = uint32_t(meta);
+                    pl.img_bytes = uint32_t(img);
+                    pl.xi = xi;
+                    pl.ring = force_ring == 4 ? 4u : 2u;
+                    pl.lds = lds;
+                }
+            }
+        }
+    }
+    return pl;
+}
+
+size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a) {
+    if (pl.ns <= 1) return 0;
+    return size_t(pl.ns - 1) * a.batch * a.rows * sizeof(unsigned long long);
+}
+
+hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial, uint32_t epoch,
+                              hipStream_t stream) {
+    if (pl.kw == 0) return hipErrorInvalidValue;
+    if (pl.ns > 1 && partial == nullptr) return hipErrorInvalidValue;
+    BandParams p;
+    p.w = a.w;
+    p.s = a.s;
+    p.b = a.b;
+    p.x = a.x;
+    p.y = a.y;
+    p.r = a.residual;
+    p.partial = partial;
+    p.epoch = epoch;
+    p.spin_limit = 1u << 22;
+    p.rows = a.rows;
+    p.cols = a.cols;
+    p.w_bytes = uint32_t(uint64_t(a.rows) * a.cols * a.bits / 8);
+    p.m_bytes = uint32_t(uint64_t(a.rows) * (a.cols / a.group) * (a.meta == Meta::F32 ? 4 : 2));
+    p.tr = pl.tr;
+    p.kw = pl.kw;
+    p.ns = pl.ns;
+    p.nbands = pl.nbands;
+    p.n_entries = pl.n_entries;
+    p.tiles = pl.tiles;
+    p.align_e = pl.align_e;
+    p.gp = pl.gp;
+    p.meta_bytes = pl.meta_bytes;
+    p.img_bytes = pl.img_bytes;
+    const int meta = static_cast<int>(a.meta);
+    if (a.bits == 4) {
+        if (meta == 0) return launch_meta<4, 0>(p, pl, a.group, a.batch, stream);
+        if (meta == 1) return launch_meta<4, 1>(p, pl, a.group, a.batch, stream);
+        return launch_meta<4, 2>(p, pl, a.group, a.batch, stream);
+    }
+    if (meta == 0) return launch_meta<8, 0>(p, pl, a.group, a.batch, stream);
+    if (meta == 1) return launch_meta<8, 1>(p, pl, a.group, a.batch, stream);
+    return launch_meta<8, 2>(p, pl, a.group, a.batch, stream);
+}
+
+}  // namespace qmr

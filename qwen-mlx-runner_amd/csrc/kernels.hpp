@@ -110,6 +110,37 @@ RowsPlan plan_affine_rows(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                           uint32_t force_kw = 0, uint32_t force_j = 0);
 hipError_t launch_affine_rows(const AffineArgs &a, const RowsPlan &pl, hipStream_t stream);
 
+// Streaming GEMV / small block on the matrix cores over row bands of 16-row
+// tiles: each band's K range in ns long splits across workgroups and KW
+// contiguous per-wave runs inside one; the band's last split adds the
+// others' epoch-tagged partial sums. See affine_tile.hip.
+struct TilePlan {
+    uint32_t kw = 0;          // waves per row tile; 0 = unsupported
+    uint32_t tr = 0;          // row tiles per band (workgroup)
+    uint32_t ns = 0;          // K splits across workgroups
+    uint32_t nbands = 0;      // row bands
+    uint32_t n_entries = 0;   // 128-byte entries per row
+    uint32_t tiles = 0;       // 128-column K tiles
+    uint32_t align_e = 0;     // split boundaries are multiples of this many entries
+    uint32_t gp = 0;          // LDS pitch of a row's metadata
+    uint32_t meta_bytes = 0;  // LDS bytes of the staged metadata
+    uint32_t img_bytes = 0;   // LDS bytes of the staged x images
+    uint32_t xi = 0;          // x items staged per thread
+    uint32_t ring = 0;        // code entries in flight per wave (2 or 4)
+    size_t lds = 0;           // dynamic LDS bytes per workgroup
+};
+bool affine_tile_supported(const AffineArgs &a);
+// Zeros leave the choice to the planner.
+TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_kw = 0,
+                          uint32_t force_tr = 0, uint32_t force_ns = 0, uint32_t force_ring = 0);
+// Workspace bytes for the partial-sum slots (0 when ns == 1).
+size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a);
+// `partial` holds affine_tile_workspace bytes (64-bit slots, any contents:
+// a slot counts only when its epoch matches); `epoch` must differ from the
+// previous launch's that used the same slots.
+hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial,
+                              uint32_t epoch, hipStream_t stream);
+
 // Wide block on MFMA (Q4/g64, F32 or BF16 metadata, batch up to 256): a prep
 // launch converts x into per-group images in `workspace` (wide_mfma_workspace
 // bytes), then the contraction launch. See wide_mfma.hip.

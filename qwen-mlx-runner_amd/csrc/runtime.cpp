@@ -42,6 +42,12 @@ struct qmr_device {
     size_t ws_partial_bytes = 0;
     uint32_t *ws_counters = nullptr;
     size_t ws_counter_count = 0;
+    // Workspace of the row-band kernel's split sums: 64-bit {value, epoch}
+    // slots (contents need no clearing: a slot counts only when its epoch is
+    // the launch's), and the epoch of the last launch.
+    unsigned long long *ws_slots = nullptr;
+    size_t ws_slots_bytes = 0;
+    uint32_t band_epoch = 0;
     // Workspace of the wide-block kernel: the activation images.
     unsigned char *ws_wide = nullptr;
     size_t ws_wide_bytes = 0;
@@ -242,8 +248,48 @@ bool rows_preferred(const qmr::MfmaPlan &pl) {
 // A forced plan (testing hook) of rr > 0 or rr == -1 selects the vector-ALU
 // tilings, rr == -3 the row-owning matrix-core kernel, rr == -2 the split-K
 // kernel whatever its shape (with ks > 0 splits, when that count is feasible).
+// The row-band kernel's plan, honouring a forced shape (rr == -4, ks =
+// ring*100000 + ns*10000 + tr*100 + kw; zero fields leave them to its
+// planner).
+qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a) {
+    const qmr::GemvPlan f = dev->forced_plan;
+    if (f.rr == -4 && f.ks > 0)
+        return qmr::plan_affine_tile(a, dev->limits, uint32_t(f.ks % 100), uint32_t(f.ks / 100 % 100),
+                                     uint32_t(f.ks / 10000 % 10), uint32_t(f.ks / 100000));
+    return qmr::plan_affine_tile(a, dev->limits);
+}
+
+// Launch the row-band kernel: grow the slot workspace when needed (after the
+// stream drains, since queued launches may use the old one) and advance the
+// launch epoch. When the epoch wraps, the slots are cleared so that no stale
+// slot can carry the new epoch.
+hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::TilePlan &pl) {
+    const size_t need = qmr::affine_tile_workspace(pl, a);
+    if (need > dev->ws_slots_bytes) {
+        check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+        if (dev->ws_slots) hipFree(dev->ws_slots);
+        dev->ws_slots = nullptr;
+        dev->ws_slots_bytes = 0;
+        const size_t n = need < (size_t(1) << 20) ? (size_t(1) << 20) : need;
+        check_hip(hipMalloc(&dev->ws_slots, n), "hipMalloc (band workspace)");
+        check_hip(hipMemsetAsync(dev->ws_slots, 0, n, dev->stream), "hipMemsetAsync (band workspace)");
+        dev->ws_slots_bytes = n;
+    }
+    if (++dev->band_epoch == 0) {
+        if (dev->ws_slots)
+            check_hip(hipMemsetAsync(dev->ws_slots, 0, dev->ws_slots_bytes, dev->stream),
+                      "hipMemsetAsync (band workspace)");
+        dev->band_epoch = 1;
+    }
+    return qmr::launch_affine_tile(a, pl, dev->ws_slots, dev->band_epoch, dev->stream);
+}
+
 hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
     const qmr::GemvPlan f = dev->forced_plan;
+    if (f.rr == -4 && qmr::affine_tile_supported(a)) {
+        const qmr::TilePlan pl = forced_tile_plan(dev, a);
+        if (pl.kw > 0) return launch_band(dev, a, pl);
+    }
     if (f.rr == -3 && qmr::affine_rows_supported(a)) {
         const qmr::RowsPlan pl = forced_rows_plan(dev, a);
         if (pl.rt > 0) return qmr::launch_affine_rows(a, pl, dev->stream);
@@ -329,6 +375,7 @@ void qmr_device_close(qmr_device *device) {
     }
     if (device->ws_partial) hipFree(device->ws_partial);
     if (device->ws_wide) hipFree(device->ws_wide);
+    if (device->ws_slots) hipFree(device->ws_slots);
     if (device->ws_counters) hipFree(device->ws_counters);
     for (int i = 0; i < 2; ++i) {
         if (device->pin[i]) hipHostFree(device->pin[i]);
@@ -877,6 +924,15 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
         a.batch = batch;
         a.meta = qmr::Meta::BF16;
         const qmr::GemvPlan f = device->forced_plan;
+        if (f.rr == -4 && qmr::affine_tile_supported(a)) {
+            const qmr::TilePlan pl = forced_tile_plan(device, a);
+            if (pl.kw > 0) {
+                // Row-band kernel: rr = -4, ks = ring*100000 + ns*10000 + tr*100 + kw.
+                if (rr) *rr = -4;
+                if (ks) *ks = int(pl.ring * 100000 + pl.ns * 10000 + pl.tr * 100 + pl.kw);
+                return QMR_OK;
+            }
+        }
         if (f.rr == -3 && qmr::affine_rows_supported(a)) {
             const qmr::RowsPlan pl = forced_rows_plan(device, a);
             if (pl.rt > 0) {
