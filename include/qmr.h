@@ -185,9 +185,10 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  */
 
 /* ---- Testing and tuning hooks (no counterpart in the reference). ---- */
-/* Force the GEMV kernel and tiling; 0,0 = planner (the split-K matrix-core
- * kernel where supported, the row-owning one past one round of resident
- * workgroups or for splits under four K tiles, else the vector-ALU kernels).
+/* Force the GEMV kernel and tiling; 0,0 = planner (the row-band matrix-core
+ * kernel where it has a one-round plan, else the split-K matrix-core kernel
+ * where supported, the row-owning one past one round of resident workgroups
+ * or for splits under four K tiles, else the vector-ALU kernels).
  *   rr = -3: row-owning matrix-core kernel (also the MLP form's); ks =
  *            j*10000 + rt*100 + kw pins its workgroup shape (rt row tiles x
  *            kw K waves) and, when j > 0, the entries per wave per staged
@@ -199,16 +200,26 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *            the row-slot tiling).
  *   rr > 0 with ks > 0: the vector-ALU row-slot kernel with `rr` rows per
  *            slot and a K-split of `ks`.
+ *   rr = -4: row-band matrix-core kernel (the default where it has a plan
+ *            whose workgroups are all resident at once); ks = ring*100000 +
+ *            ns*10000 + tr*100 + kw pins its ring depth (2 or 4), K splits,
+ *            row tiles per band and waves per tile; zero fields and ks = 0
+ *            leave them to its planner.
  * Shapes a forced kernel does not support fall back to the next one; pairs
  * that are not compiled fall back to the planner. */
 int qmr_set_gemv_plan(qmr_device *device, int rr, int ks);
 /* The plan the GEMV launcher uses for a shape with group 64 and BF16
  * metadata (honours a forced plan), in the encoding of qmr_set_gemv_plan;
- * the split-K kernel reports rr = -2 with ks = its K splits. */
+ * the row-band kernel reports rr = -4 with its ks, the split-K kernel
+ * rr = -2 with ks = its K splits. */
 int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32_t bits,
                   uint32_t batch, int *rr, int *ks);
 /* Reference pipeline label selected by the last successful qmr_encode. */
 const char *qmr_last_kernel(const qmr_device *device);
+/* The HIP kernel the last qmr_encode launched (with the row-band kernel's
+ * plan: "affine_band_kernel ring=R ns=S tr=T kw=K"), or the encode name for
+ * families with a single kernel. */
+const char *qmr_last_hip_kernel(const qmr_device *device);
 /* LDS bytes one workgroup may allocate on this device. */
 size_t qmr_device_max_lds(const qmr_device *device);
 

@@ -40,9 +40,12 @@
 // the workgroup writes NaN and exits, so every wave always finishes.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "kernels.hpp"
 #include "mfma_common.hpp"
@@ -454,6 +457,77 @@ uint32_t host_split_begin(uint32_t s, uint32_t ns, uint32_t n_entries, uint32_t 
     return a < n_entries ? a : n_entries;
 }
 
+// The plain form's kernel instance for a format, x-item count and ring
+// depth, for occupancy queries.
+template <int BITS, int META, int GROUP>
+const void *instance_group(uint32_t batch, uint32_t xi, uint32_t ring) {
+    constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
+    auto pick = [&](auto bconst) -> const void * {
+        constexpr int B = decltype(bconst)::value;
+        if (xi <= 4)
+            return ring >= 4 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 4, false>)
+                             : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 2, false>);
+        return ring >= 4 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 4, false>)
+                         : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 2, false>);
+    };
+    switch (batch) {
+        case 1: return pick(std::integral_constant<int, 1>{});
+        case 2: return pick(std::integral_constant<int, 2>{});
+        case 3:
+            if constexpr (MAXB >= 3) return pick(std::integral_constant<int, 3>{});
+            break;
+        case 4:
+            if constexpr (MAXB >= 4) return pick(std::integral_constant<int, 4>{});
+            break;
+        default: break;
+    }
+    return nullptr;
+}
+
+template <int BITS, int META>
+const void *instance_meta(uint32_t group, uint32_t batch, uint32_t xi, uint32_t ring) {
+    switch (group) {
+        case 32: return instance_group<BITS, META, 32>(batch, xi, ring);
+        case 64: return instance_group<BITS, META, 64>(batch, xi, ring);
+        case 128: return instance_group<BITS, META, 128>(batch, xi, ring);
+        default: return nullptr;
+    }
+}
+
+const void *instance(const AffineArgs &a, uint32_t xi, uint32_t ring) {
+    const int meta = static_cast<int>(a.meta);
+    if (a.bits == 4) {
+        if (meta == 0) return instance_meta<4, 0>(a.group, a.batch, xi, ring);
+        if (meta == 1) return instance_meta<4, 1>(a.group, a.batch, xi, ring);
+        return instance_meta<4, 2>(a.group, a.batch, xi, ring);
+    }
+    if (meta == 0) return instance_meta<8, 0>(a.group, a.batch, xi, ring);
+    if (meta == 1) return instance_meta<8, 1>(a.group, a.batch, xi, ring);
+    return instance_meta<8, 2>(a.group, a.batch, xi, ring);
+}
+
+// Resident workgroups per CU for an instance, block size and dynamic LDS,
+// as the runtime computes them from registers and LDS; cached.
+uint32_t resident_per_cu(const void *kernel, uint32_t threads, size_t lds) {
+    struct Entry {
+        const void *k;
+        uint32_t threads;
+        size_t lds;
+        uint32_t n;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry &e : cache)
+        if (e.k == kernel && e.threads == threads && e.lds == lds) return e.n;
+    int n = 0;
+    if (kernel == nullptr ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, int(threads), lds) != hipSuccess || n < 1)
+        n = 1;
+    cache.push_back(Entry{kernel, threads, lds, uint32_t(n)});
+    return uint32_t(n);
+}
+
 }  // namespace
 
 bool affine_tile_supported(const AffineArgs &a) {
@@ -483,66 +557,72 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     const uint32_t align_e = std::max(1u, 16u / (mb * tpe * ngm));
     const uint32_t cus = lim.num_cus > 0 ? uint32_t(lim.num_cus) : 256u;
     const size_t timg = size_t(4) * 4 * 2 * a.batch * 16 + size_t(ngm) * ((16 / ngm / 2) / 2) * 16;
-    // Candidate shapes: tr tiles per band, ns K splits, kw waves per tile.
-    // Score (fitted to the read-pattern measurements): workgroups near one
-    // per CU or more but no more than resident, about 1.5-2 waves per SIMD,
-    // rows per band as many as that allows (x traffic), few splits.
+    const double wbytes = double(a.rows) * row_bytes + 2.0 * a.rows * (a.cols / a.group) * mb;
+    // Candidates: ring depth, K splits, tiles per band, waves per tile. Every
+    // workgroup must be resident in one round (a second round repeats the
+    // start-up latency). Score, fitted to timings of 160 shapes at
+    // 5120x17408 and 17408x5120 (B=1 and B=3) on MI355X:
+    //   0.5 |log2(waves / two per SIMD)|
+    //   + log2(workgroups per CU rounded up / the even share)
+    //   + x bytes read from L2 (once per band) / weight bytes
+    //   + 0.2 for a two-entry ring.
     double best = 1e30;
-    for (uint32_t tr : {1u, 2u, 4u, 8u}) {
-        if (force_tr && tr != force_tr) continue;
-        if (tr > row_tiles && tr > 1) continue;
-        const uint32_t nbands = (row_tiles + tr - 1) / tr;
-        for (uint32_t ns : {1u, 2u, 3u, 4u}) {
+    for (uint32_t ring : {2u, 4u}) {
+        if (force_ring && ring != force_ring) continue;
+        for (uint32_t ns = 1; ns <= 4; ++ns) {
             if (force_ns && ns != force_ns) continue;
             if (ns * align_e > n_entries) continue;
-            // The largest split (entries) after alignment.
             uint32_t max_se = 0;
-            for (uint32_t s = 0; s < ns; ++s) {
-                const uint32_t e0 = host_split_begin(s, ns, n_entries, align_e);
-                const uint32_t e1 = host_split_begin(s + 1, ns, n_entries, align_e);
-                if (e1 <= e0) max_se = 0x7FFFFFFF;
+            bool empty = false;
+            for (uint32_t sp = 0; sp < ns; ++sp) {
+                const uint32_t e0 = host_split_begin(sp, ns, n_entries, align_e);
+                const uint32_t e1 = host_split_begin(sp + 1, ns, n_entries, align_e);
+                if (e1 <= e0) empty = true;
                 else max_se = std::max(max_se, e1 - e0);
             }
-            if (max_se == 0x7FFFFFFF) continue;
+            if (empty) continue;
             const uint32_t max_tiles = std::min(max_se * tpe, tiles);
-            for (uint32_t kw : {1u, 2u, 4u, 8u}) {
-                if (force_kw && kw != force_kw) continue;
-                const uint32_t threads = tr * kw * 64;
-                if (threads > uint32_t(kMaxThreads) || kw > max_se) continue;
-                const uint32_t items = max_tiles * a.batch * 16;
-                const uint32_t xi = (items + threads - 1) / threads;
-                if (xi > 8) continue;
-                const uint32_t gp = (max_tiles * ngm) | 1u;
-                const size_t meta = (size_t(tr) * 16 * gp * 4 * (a.meta == Meta::F32 ? 2 : 1) + 15) & ~size_t(15);
-                const size_t img = size_t(max_tiles) * timg;
-                const size_t lds = meta + img + size_t(tr * kw) * a.batch * 16 * 4;
-                if (lds > lim.max_lds_per_block) continue;
-                const double wgs = double(nbands) * ns;
-                const double waves = wgs * tr * kw;
-                // Workgroups per CU rounded up, against the even share.
-                const double per_cu = std::ceil(wgs / cus) / (wgs / cus);
-                double score = std::fabs(std::log(waves / (1.5 * 4 * cus)));
-                if (wgs < 0.6 * cus) score += 2.0 * std::log(0.6 * cus / wgs);
-                score += 0.5 * std::log(per_cu);
-                score += 0.15 * (ns - 1);
-                // x read from L2 once per band, relative to the weight bytes.
-                const double wbytes = double(a.rows) * row_bytes + 2.0 * a.rows * (a.cols / a.group) * mb;
-                score += 2.0 * double(nbands) * a.batch * a.cols * 4.0 / wbytes;
-                if (score < best - 1e-9 || (force_kw && force_tr && force_ns)) {
-                    best = score;
-                    pl.kw = kw;
-                    pl.tr = tr;
-                    pl.ns = ns;
-                    pl.nbands = nbands;
-                    pl.n_entries = n_entries;
-                    pl.tiles = tiles;
-                    pl.align_e = align_e;
-                    pl.gp = gp;
-                    pl.meta_bytes = uint32_t(meta);
-                    pl.img_bytes = uint32_t(img);
-                    pl.xi = xi;
-                    pl.ring = force_ring == 4 ? 4u : 2u;
-                    pl.lds = lds;
+            for (uint32_t tr : {1u, 2u, 4u, 8u}) {
+                if (force_tr && tr != force_tr) continue;
+                if (tr > 1 && (tr / 2) * 16 >= a.rows) continue;
+                const uint32_t nbands = (row_tiles + tr - 1) / tr;
+                for (uint32_t kw : {1u, 2u, 4u, 8u}) {
+                    if (force_kw && kw != force_kw) continue;
+                    const uint32_t threads = tr * kw * 64;
+                    if (threads > uint32_t(kMaxThreads) || kw > max_se) continue;
+                    const uint32_t items = max_tiles * a.batch * 16;
+                    const uint32_t xi = (items + threads - 1) / threads;
+                    if (xi > 8) continue;
+                    const uint32_t gp = (max_tiles * ngm) | 1u;
+                    const size_t meta = (size_t(tr) * 16 * gp * 4 * (a.meta == Meta::F32 ? 2 : 1) + 15) & ~size_t(15);
+                    const size_t img = size_t(max_tiles) * timg;
+                    const size_t lds = meta + img + size_t(tr * kw) * a.batch * 16 * 4;
+                    if (lds > lim.max_lds_per_block) continue;
+                    const double wgs = double(nbands) * ns;
+                    const uint32_t resident = resident_per_cu(instance(a, xi, ring), threads, lds);
+                    if (wgs > double(resident) * cus) continue;
+                    const double waves = wgs * tr * kw;
+                    const double per_cu = std::ceil(wgs / cus) / (wgs / cus);
+                    double score = 0.5 * std::fabs(std::log2(waves / (2.0 * 4 * cus)));
+                    score += std::log2(per_cu);
+                    score += double(nbands) * a.batch * a.cols * 4.0 / wbytes;
+                    score += ring == 2 ? 0.2 : 0.0;
+                    if (score < best - 1e-9) {
+                        best = score;
+                        pl.kw = kw;
+                        pl.tr = tr;
+                        pl.ns = ns;
+                        pl.nbands = nbands;
+                        pl.n_entries = n_entries;
+                        pl.tiles = tiles;
+                        pl.align_e = align_e;
+                        pl.gp = gp;
+                        pl.meta_bytes = uint32_t(meta);
+                        pl.img_bytes = uint32_t(img);
+                        pl.xi = xi;
+                        pl.ring = ring;
+                        pl.lds = lds;
+                    }
                 }
             }
         }

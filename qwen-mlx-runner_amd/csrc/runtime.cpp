@@ -10,6 +10,7 @@
 #include <cstring>
 #include <string>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/qmr.h"
@@ -36,6 +37,7 @@ struct qmr_device {
     // rr > 0: vector-ALU kernels.
     qmr::GemvPlan forced_plan;
     std::string last_kernel;    // selected reference pipeline label
+    std::string last_hip;       // HIP kernel (and plan) of the last launch
     // Workspace of the split-K matrix-core kernel's cross-workgroup reduction:
     // partial sums and per-band arrival counters (kept zero between launches).
     float *ws_partial = nullptr;
@@ -48,6 +50,9 @@ struct qmr_device {
     unsigned long long *ws_slots = nullptr;
     size_t ws_slots_bytes = 0;
     uint32_t band_epoch = 0;
+    // Row-band plans by shape, format and forced plan: planning enumerates
+    // ~100 shapes with occupancy queries, which must not sit on every launch.
+    mutable std::unordered_map<uint64_t, qmr::TilePlan> band_plans;
     // Workspace of the wide-block kernel: the activation images.
     unsigned char *ws_wide = nullptr;
     size_t ws_wide_bytes = 0;
@@ -242,21 +247,25 @@ bool rows_preferred(const qmr::MfmaPlan &pl) {
     return pl.rounds > 1 || (pl.ns > 1 && pl.tps < 4);
 }
 
-// One packed-affine product of at most four RHS: the split-K matrix-core
-// kernel where it supports the format, unless rows_preferred() hands the
-// shape to the row-owning matrix-core kernel; else the vector-ALU kernels.
-// A forced plan (testing hook) of rr > 0 or rr == -1 selects the vector-ALU
-// tilings, rr == -3 the row-owning matrix-core kernel, rr == -2 the split-K
-// kernel whatever its shape (with ks > 0 splits, when that count is feasible).
 // The row-band kernel's plan, honouring a forced shape (rr == -4, ks =
 // ring*100000 + ns*10000 + tr*100 + kw; zero fields leave them to its
 // planner).
 qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a) {
     const qmr::GemvPlan f = dev->forced_plan;
-    if (f.rr == -4 && f.ks > 0)
-        return qmr::plan_affine_tile(a, dev->limits, uint32_t(f.ks % 100), uint32_t(f.ks / 100 % 100),
-                                     uint32_t(f.ks / 10000 % 10), uint32_t(f.ks / 100000));
-    return qmr::plan_affine_tile(a, dev->limits);
+    const int ks = f.rr == -4 ? f.ks : 0;
+    uint64_t key = (uint64_t(a.rows) << 32) | a.cols;
+    key = key * 1000003u ^ (uint64_t(a.bits) << 24 | uint64_t(a.group) << 12 | uint64_t(a.batch) << 4 |
+                            uint64_t(static_cast<int>(a.meta)) << 1 | (a.residual ? 1u : 0u));
+    key = key * 1000003u ^ uint64_t(uint32_t(ks));
+    const auto it = dev->band_plans.find(key);
+    if (it != dev->band_plans.end()) return it->second;
+    const qmr::TilePlan pl =
+        ks > 0 ? qmr::plan_affine_tile(a, dev->limits, uint32_t(ks % 100), uint32_t(ks / 100 % 100),
+                                       uint32_t(ks / 10000 % 10), uint32_t(ks / 100000))
+               : qmr::plan_affine_tile(a, dev->limits);
+    if (dev->band_plans.size() > 4096) dev->band_plans.clear();
+    dev->band_plans.emplace(key, pl);
+    return pl;
 }
 
 // Launch the row-band kernel: grow the slot workspace when needed (after the
@@ -281,33 +290,52 @@ hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::Til
                       "hipMemsetAsync (band workspace)");
         dev->band_epoch = 1;
     }
+    dev->last_hip = "affine_band_kernel ring=" + std::to_string(pl.ring) + " ns=" + std::to_string(pl.ns) +
+                    " tr=" + std::to_string(pl.tr) + " kw=" + std::to_string(pl.kw);
     return qmr::launch_affine_tile(a, pl, dev->ws_slots, dev->band_epoch, dev->stream);
 }
 
+// One packed-affine product of at most four RHS: the row-band matrix-core
+// kernel where it has a plan whose workgroups are all resident at once; else
+// the split-K matrix-core kernel where it supports the format, unless
+// rows_preferred() hands the shape to the row-owning matrix-core kernel;
+// else the vector-ALU kernels. A forced plan (testing hook) of rr > 0 or
+// rr == -1 selects the vector-ALU tilings, rr == -4 the row-band kernel,
+// rr == -3 the row-owning matrix-core kernel, rr == -2 the split-K kernel
+// whatever its shape (with ks > 0 splits, when that count is feasible).
 hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
-    const qmr::GemvPlan f = dev->forced_plan;
-    if (f.rr == -4 && qmr::affine_tile_supported(a)) {
+    qmr::GemvPlan f = dev->forced_plan;
+    if ((f.rr == 0 || f.rr == -4) && qmr::affine_tile_supported(a)) {
         const qmr::TilePlan pl = forced_tile_plan(dev, a);
         if (pl.kw > 0) return launch_band(dev, a, pl);
     }
+    if (f.rr == -4) f = qmr::GemvPlan{};  // no band plan for this shape: the default chain
     if (f.rr == -3 && qmr::affine_rows_supported(a)) {
         const qmr::RowsPlan pl = forced_rows_plan(dev, a);
-        if (pl.rt > 0) return qmr::launch_affine_rows(a, pl, dev->stream);
+        if (pl.rt > 0) {
+            dev->last_hip = "affine_rows_kernel";
+            return qmr::launch_affine_rows(a, pl, dev->stream);
+        }
     }
     if ((f.rr == 0 || f.rr == -2 || f.rr == -3) && qmr::affine_mfma_supported(a)) {
         const qmr::MfmaPlan pl =
             qmr::plan_affine_mfma(a, dev->limits, f.rr == -2 && f.ks > 0 ? uint32_t(f.ks) : 0u);
         if (f.rr == 0 && pl.rt > 0 && rows_preferred(pl) && qmr::affine_rows_supported(a)) {
             const qmr::RowsPlan rp = qmr::plan_affine_rows(a, dev->limits);
-            if (rp.rt > 0) return qmr::launch_affine_rows(a, rp, dev->stream);
+            if (rp.rt > 0) {
+                dev->last_hip = "affine_rows_kernel";
+                return qmr::launch_affine_rows(a, rp, dev->stream);
+            }
         }
         if (pl.rt > 0) {
             ensure_workspace(dev, qmr::affine_mfma_workspace(pl, a), pl.nbands);
+            dev->last_hip = "affine_mfma_kernel";
             return qmr::launch_affine_mfma(a, pl, dev->ws_partial, dev->ws_counters, dev->stream);
         }
     }
     // The vector-ALU kernels have no fused epilogue.
     ensure(a.residual == nullptr, "fused product needs a matrix-core kernel", QMR_ERR_UNSUPPORTED);
+    dev->last_hip = "affine_gemv_kernel";
     return qmr::launch_affine_gemv(a, f.rr < -1 ? qmr::GemvPlan{} : f, dev->limits, dev->stream);
 }
 
@@ -719,6 +747,7 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                name + ": invalid threadgroup size " + std::to_string(group_size));
 
         dev->last_kernel = label ? label : name;
+        dev->last_hip = name;  // the families below name their own kernel
         check_hip(hipSetDevice(dev->ordinal), "hipSetDevice");
         auto ptr = [&](size_t i) -> char * {
             return static_cast<char *>(buffers[i]->ptr) + off(i);
@@ -772,6 +801,7 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                 const qmr::MfmaPlan mp = qmr::plan_affine_mfma(a, dev->limits);
                 if (f.rr != -3 && mp.rt > 0) {
                     ensure_workspace(dev, qmr::affine_mfma_workspace(mp, a), mp.nbands);
+                    dev->last_hip = "affine_mfma_kernel (MLP)";
                     e = qmr::launch_affine_mfma(a, mp, dev->ws_partial, dev->ws_counters, dev->stream);
                 } else {
                     const qmr::RowsPlan pl =
@@ -780,6 +810,7 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                                                    uint32_t(f.ks / 10000))
                             : qmr::plan_affine_mlp(a, dev->limits);
                     ensure(pl.rt > 0, name + ": no fused tiling for this shape", QMR_ERR_UNSUPPORTED);
+                    dev->last_hip = "affine_rows_kernel (MLP)";
                     e = qmr::launch_affine_rows(a, pl, dev->stream);
                 }
             } else {
@@ -817,6 +848,7 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                     check_hip(hipMalloc(&dev->ws_wide, need), "hipMalloc (wide workspace)");
                     dev->ws_wide_bytes = need;
                 }
+                dev->last_hip = "wide_mfma_kernel";
                 e = qmr::launch_wide_mfma(a, dev->ws_wide, dev->limits, dev->stream);
             } else if (wide) {
                 // Wide blocks of up to eight RHS, and those outside the wide
@@ -829,6 +861,7 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                     e = launch_product(dev, sub);
                 }
             } else if (dev->reference || !fast_group) {
+                dev->last_hip = "affine_generic_kernel";
                 e = qmr::launch_affine_generic(a, dev->stream);
             } else {
                 e = launch_product(dev, a);
@@ -912,6 +945,10 @@ const char *qmr_last_kernel(const qmr_device *device) {
     return device ? device->last_kernel.c_str() : "";
 }
 
+const char *qmr_last_hip_kernel(const qmr_device *device) {
+    return device ? device->last_hip.c_str() : "";
+}
+
 int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32_t bits,
                   uint32_t batch, int *rr, int *ks) {
     return guarded([&]() -> int {
@@ -923,8 +960,8 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
         a.group = 64;
         a.batch = batch;
         a.meta = qmr::Meta::BF16;
-        const qmr::GemvPlan f = device->forced_plan;
-        if (f.rr == -4 && qmr::affine_tile_supported(a)) {
+        qmr::GemvPlan f = device->forced_plan;
+        if ((f.rr == 0 || f.rr == -4) && qmr::affine_tile_supported(a)) {
             const qmr::TilePlan pl = forced_tile_plan(device, a);
             if (pl.kw > 0) {
                 // Row-band kernel: rr = -4, ks = ring*100000 + ns*10000 + tr*100 + kw.
@@ -933,6 +970,7 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
                 return QMR_OK;
             }
         }
+        if (f.rr == -4) f = qmr::GemvPlan{};
         if (f.rr == -3 && qmr::affine_rows_supported(a)) {
             const qmr::RowsPlan pl = forced_rows_plan(device, a);
             if (pl.rt > 0) {

@@ -42,7 +42,7 @@ EXPORTED_SYMBOLS = (
     "qmr_checked_buffer_range", "qmr_ranges_overlap", "qmr_specialized_matvec",
     "qmr_specialized_matmul", "qmr_parse_block_kernel_mode", "qmr_pack_bf16_exact",
     "qmr_supported_bf16_quantization", "qmr_set_gemv_plan", "qmr_gemv_plan",
-    "qmr_last_kernel", "qmr_device_max_lds",
+    "qmr_last_kernel", "qmr_last_hip_kernel", "qmr_device_max_lds",
     # include/qmr_checkpoint.h
     "qmr_checkpoint_open", "qmr_checkpoint_close", "qmr_checkpoint_tensor_count",
     "qmr_checkpoint_contains", "qmr_checkpoint_matrix_info", "qmr_checkpoint_matrix",
@@ -148,6 +148,7 @@ def lib() -> C.CDLL:
         "qmr_gemv_plan": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                     C.POINTER(C.c_int), C.POINTER(C.c_int)]),
         "qmr_last_kernel": (C.c_char_p, [vp]),
+        "qmr_last_hip_kernel": (C.c_char_p, [vp]),
         "qmr_device_max_lds": (sz, [vp]),
         "qmr_checkpoint_open": (C.c_int, [C.c_char_p, C.POINTER(vp)]),
         "qmr_checkpoint_close": (None, [vp]),
@@ -370,6 +371,10 @@ class Gpu:
 
     def last_kernel(self) -> str:
         return lib().qmr_last_kernel(self._h).decode()
+
+    def last_hip_kernel(self) -> str:
+        """The HIP kernel (and row-band plan) the last encode launched."""
+        return lib().qmr_last_hip_kernel(self._h).decode()
 
     def max_lds(self) -> int:
         return int(lib().qmr_device_max_lds(self._h))

@@ -232,28 +232,28 @@ def test_row_kernel_is_deterministic(gpu, rows, cols, batch):
 
 
 @pytest.mark.parametrize("rows,cols,bits,batch,kind", [
-    (5120, 17408, 4, 1, -2), (17408, 5120, 4, 3, -2), (5120, 5120, 4, 1, -2), (5120, 17408, 8, 1, -2),
-    (151936, 5120, 4, 1, -3), (151936, 5120, 4, 3, -3), (5120, 5120, 8, 1, -3), (5120, 5120, 8, 3, -3),
-    (2048, 2048, 8, 1, -3)])
-def test_default_plan_takes_row_owning_kernel_past_one_round(gpu, rows, cols, bits, batch, kind):
-    """The default planner keeps the split-K kernel while its grid fits in
-    one round of resident workgroups and each split covers at least four K
-    tiles (the Q4 and Q8 MLP shapes, a Q4 5120x5120 matrix), and takes the
-    row-owning kernel past one round (the vocabulary head) or for shorter
-    splits (the Q8 5120x5120 projection, a Q8 2048x2048 matrix)."""
+    (5120, 17408, 4, 1, -4), (17408, 5120, 4, 3, -4), (5120, 5120, 4, 1, -4), (5120, 17408, 8, 1, -4),
+    (5120, 5120, 8, 3, -4), (151936, 5120, 4, 1, -3), (151936, 5120, 4, 3, -3)])
+def test_default_plan_kernel_family(gpu, rows, cols, bits, batch, kind):
+    """The default planner takes the row-band kernel wherever it has a plan
+    whose workgroups are all resident in one round (the Q4 and Q8 MLP
+    shapes, 5120x5120 projections), and the row-owning kernel where no such
+    plan exists (the vocabulary head)."""
     gpu.set_gemv_plan(0, 0)
     plan = gpu.gemv_plan(rows, cols, bits, batch)
     assert plan[0] == kind, f"{rows}x{cols} B{batch}: expected plan kind {kind}, got {plan}"
 
 
 @pytest.mark.parametrize("rr,name,batch", [(0, "matmul_affine_bf16", 1), (0, "matmul_affine_bf16", 3),
-                                           (-3, "matmul_affine_bf16", 2), (0, "matmul_affine_wide_bf16", 100)])
+                                           (-2, "matmul_affine_bf16", 2), (-3, "matmul_affine_bf16", 2),
+                                           (0, "matmul_affine_wide_bf16", 100)])
 def test_matrix_core_kernels_read_x_at_4_byte_offsets(gpu, rr, name, batch):
     """x (and y) views 4-byte but not 16-byte aligned, as the block contract
     allows (tests/batch_matrix.rs:176-191; the BF16 matvec names require
     16-byte aligned input instead), with codes and metadata aligned so the
-    matrix-core kernels (split-K, row-owning, wide) take the product: their
-    x loads are 128-bit loads that need only 4-byte alignment."""
+    matrix-core kernels (row-band, split-K, row-owning, wide) take the
+    product: their x loads are 128-bit loads that need only 4-byte
+    alignment."""
     rows, cols = 300, 4096
     rng = np.random.default_rng(batch * 7 + (rr < 0))
     w = rng.integers(0, 2**32, rows * cols // 8, dtype=np.uint32)
@@ -266,7 +266,7 @@ def test_matrix_core_kernels_read_x_at_4_byte_offsets(gpu, rr, name, batch):
     try:
         if batch <= 4:
             plan = gpu.gemv_plan(rows, cols, 4, batch)
-            assert plan[0] in (-2, -3), f"expected a matrix-core plan, got {plan}"
+            assert plan[0] in (-2, -3, -4), f"expected a matrix-core plan, got {plan}"
         wb, sb, bb = gpu.upload_bytes(w), gpu.upload_bytes(s), gpu.upload_bytes(b)
         xb = gpu.upload_f32(np.concatenate([[99.0], x.ravel()]).astype(np.float32))
         yb = gpu.upload_f32(np.full(batch * rows + 2, 12345.0, np.float32))
@@ -303,15 +303,17 @@ def test_dense_f16_products_at_scale(gpu, rows, cols, batch):
 def test_forced_split_count_is_honoured_and_correct(gpu):
     """The tuning hook rr = -2, ks = n keeps only n K splits when feasible
     (17408x5120 at B=1: 10 splits), and the product still meets the gate;
-    an infeasible count falls back to the planner's."""
+    an infeasible count falls back to the split-K planner's own count."""
     rows, cols = synth.MLP_SHAPES["gate_up"]
-    default = gpu.gemv_plan(rows, cols, 4, 1)
-    gpu.set_gemv_plan(-2, 10)
+    gpu.set_gemv_plan(-2, 0)
     try:
+        split_k_default = gpu.gemv_plan(rows, cols, 4, 1)
+        assert split_k_default[0] == -2
+        gpu.set_gemv_plan(-2, 10)
         assert gpu.gemv_plan(rows, cols, 4, 1) == (-2, 10)
         got, want = _launch_three(gpu, rows, cols, 1, 41)
         assert_gate(got[0], want, "forced 10 splits")
         gpu.set_gemv_plan(-2, 31)
-        assert gpu.gemv_plan(rows, cols, 4, 1) == default
+        assert gpu.gemv_plan(rows, cols, 4, 1) == split_k_default
     finally:
         gpu.set_gemv_plan(0, 0)
