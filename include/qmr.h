@@ -177,6 +177,12 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *     Buffers gate w/s/b, up w/s/b (same shape and format), x [batch][cols],
  *     norm [cols], y [batch][rows]; params rows, cols, bits, group, batch
  *     (1..4), eps as FP32 bits (finite, positive). Matrix-core formats only.
+ *   "read_checksum"
+ *     One streaming read of three byte views: buffers a, b, c, out; params
+ *     the three sizes in bytes (multiples of 4, not all zero); threads =
+ *     ceil((a+b+c)/16). out holds 4096 u32 slots whose XOR is the XOR of
+ *     every 32-bit word read. The read floor of a product's codes and
+ *     metadata, for measurement; it computes nothing else.
  *   "matvec_affine_f16meta", "matmul_affine_f16meta", "embed_affine_f16meta"
  *     As the FP32-metadata names, with scales/biases stored as IEEE binary16
  *     (the dtype MLX checkpoints ship). The reference expands F16 metadata

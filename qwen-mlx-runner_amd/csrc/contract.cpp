@@ -95,6 +95,8 @@ Layout dispatch_layout(const std::string &name, const uint32_t *p, size_t np) {
     size_t count;
     if (name == "copy_f32") {
         count = 1;
+    } else if (name == "read_checksum") {
+        count = 3;
     } else if (name == "matvec_f16" || name == "embed_f16") {
         count = 2;
     } else if (name == "matvec_affine" || name == "embed_affine" || name == "matvec_affine_bf16" ||
@@ -131,6 +133,21 @@ Layout dispatch_layout(const std::string &name, const uint32_t *p, size_t np) {
     const Meta meta = meta_of_name(name);
     const size_t meta_bytes_per = meta == Meta::F32 ? 4 : 2;
     Layout out;
+
+    // read_checksum [a, b, c] (byte sizes, multiples of 4, not all zero) ->
+    // views of a, b and c bytes and the checksum slots; one thread per 16
+    // bytes read. A library addition: the read floor of the GEMV's bytes.
+    if (name == "read_checksum") {
+        size_t total = 0;
+        for (size_t i = 0; i < 3; ++i) {
+            ensure(p[i] % 4 == 0, name + ": view sizes must be multiples of 4 bytes");
+            total += p[i];
+        }
+        ensure(total > 0, name + ": dimensions must be nonzero");
+        out.sizes = {n(0), n(1), n(2), size_t(kChecksumSlots) * 4};
+        out.threads = (total + 15) / 16;
+        return out;
+    }
 
     // src/gpu.rs:1173-1176: copy_f32 [n] -> two views of n floats, n threads.
     if (name == "copy_f32") {

@@ -82,5 +82,8 @@ bool is_wide_name(const std::string &name);           // matmul_affine_wide*
 bool is_residual_name(const std::string &name);
 bool is_mlp_name(const std::string &name);
 bool is_fused_name(const std::string &name);
+// read_checksum: u32 checksum slots written per launch (the XOR of all of
+// them is the XOR of every 32-bit word read).
+constexpr uint32_t kChecksumSlots = 4096;
 
 }  // namespace qmr

@@ -692,7 +692,7 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
         // (the in-place x += W a of a decoder layer).
         const bool fused = qmr::is_fused_name(name);
         ensure(!dev->reference || !fused, "Fused dispatch is unavailable in reference mode");
-        if (qmr::starts_with(name, "matmul_") || name == "copy_f32" || fused) {
+        if (qmr::starts_with(name, "matmul_") || name == "copy_f32" || name == "read_checksum" || fused) {
             const size_t out = nbuffers - 1;
             for (size_t i = 0; i < out; ++i) {
                 if (buffers[i] == buffers[out]) {
@@ -757,6 +757,9 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
             e = qmr::launch_embed_affine(reinterpret_cast<const uint32_t *>(ptr(0)), ptr(1), ptr(2),
                                          meta, params[0], params[1], params[2], params[3],
                                          reinterpret_cast<float *>(ptr(3)), dev->stream);
+        } else if (name == "read_checksum") {
+            e = qmr::launch_read_checksum(ptr(0), params[0], ptr(1), params[1], ptr(2), params[2],
+                                          reinterpret_cast<uint32_t *>(ptr(3)), dev->stream);
         } else if (name == "copy_f32") {
             e = qmr::launch_copy_f32(reinterpret_cast<const float *>(ptr(0)),
                                      reinterpret_cast<float *>(ptr(1)), params[0], dev->limits.num_cus,

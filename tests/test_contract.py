@@ -121,6 +121,13 @@ def test_batch_dispatch_layout_sizes_all_rhs_and_rejects_invalid_batches():
     err(qmr.dispatch_layout, "matmul_f16", [1, U32_MAX, 4])
     assert qmr.dispatch_layout("copy_f32", [7]) == ([28, 28], 7)
     err(qmr.dispatch_layout, "copy_f32", [0])
+    # The read-floor name (a library addition): three byte views, one thread
+    # per 16 bytes, 4096 u32 checksum slots.
+    assert qmr.dispatch_layout("read_checksum", [44, 8, 0]) == ([44, 8, 0, 16384], 4)
+    assert qmr.dispatch_layout("read_checksum", [16, 16, 16]) == ([16, 16, 16, 16384], 3)
+    err(qmr.dispatch_layout, "read_checksum", [0, 0, 0])
+    err(qmr.dispatch_layout, "read_checksum", [6, 0, 0])
+    err(qmr.dispatch_layout, "read_checksum", [16, 16])
 
 
 # src/gpu.rs:1568-1582

@@ -317,3 +317,27 @@ def test_forced_split_count_is_honoured_and_correct(gpu):
         assert gpu.gemv_plan(rows, cols, 4, 1) == split_k_default
     finally:
         gpu.set_gemv_plan(0, 0)
+
+
+@pytest.mark.parametrize("sizes,offsets", [((44_564_480, 2_785_280, 2_785_280), (0, 0, 0, 0)),
+                                           ((1_000_004, 36, 0), (4, 0, 0, 0)),
+                                           ((20, 1_048_576, 4), (0, 8, 12, 4))])
+def test_read_checksum_reads_every_word_once(gpu, sizes, offsets):
+    """read_checksum (the read-floor kernel): the XOR of its slots equals the
+    XOR of every 32-bit word of the three views, for word tails that are not
+    16-byte multiples, an empty view and 4-byte view offsets."""
+    rng = np.random.default_rng(sum(sizes))
+    views = [rng.integers(0, 2**32, n // 4, dtype=np.uint64).astype(np.uint32) for n in sizes]
+    bufs = []
+    for v, off in zip(views, offsets[:3]):
+        pad = np.full(off // 4, 0xDEADBEEF, np.uint32)
+        bufs.append(gpu.upload_bytes(np.concatenate([pad, v, np.full(3, 0xABCDEF01, np.uint32)])))
+    out = gpu.upload_bytes(np.full(4096 + offsets[3] // 4, 0x55555555, np.uint32))
+    for launch in range(2):
+        gpu.dispatch("read_checksum", bufs + [out], list(sizes), offsets=list(offsets))
+        slots = np.frombuffer(out.read_bytes(offsets[3], 4096 * 4), np.uint32)
+        want = np.uint32(0)
+        for v in views:
+            if v.size:
+                want ^= np.bitwise_xor.reduce(v)
+        assert np.bitwise_xor.reduce(slots) == want, f"launch {launch}"
