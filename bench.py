@@ -22,9 +22,14 @@ of building that case's matrix.
 The CPU baseline times the FP64 oracle (the reference's per-weight
 dequantise-then-accumulate closure, restated in C) on this host.
 
-BASELINE config 3 (the Q8/g64 F16 5120x5120 projection and the Q4/g64 BF16
-151936x5120 vocabulary head, B=1 and B=3) is reported under "config3" with an
-HBM roofline per case.
+The read floor: read_checksum streams the metric matrix's codes, scales and
+biases (the same rotating copies, the same timing) and does nothing else; its
+time is reported as roofline.read_floor_us and roofline.frac_of_floor is that
+time over the GEMV's.
+
+BASELINE config 3 (the Q8/g64 F16 5120x5120 projection, the same matrix with
+FP32 metadata, and the Q4/g64 BF16 151936x5120 vocabulary head, B=1 and B=3)
+is reported under "config3" with an HBM roofline per case.
 
 One decoder layer's MLP in the fused forms (RMS norm + gate + up + SwiGLU in
 one launch, down + residual add in a second) is reported under "mlp", beside
@@ -234,13 +239,14 @@ def bench_config3(gpu: qmr.Gpu, args) -> list:
     projection and the Q4/g64 BF16 151936x5120 vocabulary head, each at B=1
     and B=3. Weights rotate over enough copies to exceed the Infinity Cache
     (10 of the 26 MB projection, 2 of the 440 MB head)."""
-    cases = [("q8_proj", synth.q8_f16_matrix(5120, 5120, synth.DEFAULT_SEED, tag="q8"), 10),
+    q8 = synth.q8_f16_matrix(5120, 5120, synth.DEFAULT_SEED, tag="q8")
+    cases = [("q8_proj", q8, 10), ("q8_proj_f32meta", synth.to_f32_metadata(q8), 10),
              ("head", synth.q4_bf16_matrix(*synth.HEAD_SHAPE, synth.DEFAULT_SEED, tag="head"), 2)]
     out = []
     for tag, m, copies in cases:
         mats = [(gpu.upload_bytes(m.w), gpu.upload_bytes(m.s), gpu.upload_bytes(m.b))
                 for _ in range(copies)]
-        suffix = "_f16meta" if m.meta == "f16" else "_bf16"
+        suffix = {"f16": "_f16meta", "bf16": "_bf16", "f32": ""}[m.meta]
         for batch in (1, 3):
             x = synth.activations(m.cols, batch, synth.DEFAULT_SEED, tag="bench")
             xb = gpu.upload_f32(x.ravel())
@@ -255,7 +261,8 @@ def bench_config3(gpu: qmr.Gpu, args) -> list:
             plan = gpu.gemv_plan(m.rows, m.cols, m.bits, batch)
             r = {
                 "shape": f"{m.rows}x{m.cols}", "tag": tag, "bits": m.bits, "metadata": m.meta,
-                "batch": batch, "kernel": hip_kernel(plan), "plan": list(plan),
+                "batch": batch, "kernel": hip_kernel(plan), "hip_launch": gpu.last_hip_kernel(),
+                "plan": list(plan),
                 "us_mean": round(mean_ms * 1e3, 2), "algorithmic_bytes": nbytes,
                 "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBS, 4)},
@@ -450,9 +457,37 @@ def bench_loader(args) -> dict:
 
 
 def hip_kernel(plan) -> str:
-    """The HIP kernel family the planner picked (plan[0]: -2 split-K matrix
-    cores, -3 row-owning matrix cores, otherwise the vector-ALU kernel)."""
-    return {-2: "affine_mfma_kernel", -3: "affine_rows_kernel"}.get(plan[0], "affine_gemv_kernel")
+    """The HIP kernel family the planner picked (plan[0]: -4 row-band matrix
+    cores, -2 split-K matrix cores, -3 row-owning matrix cores, otherwise the
+    vector-ALU kernel)."""
+    return {-4: "affine_band_kernel", -2: "affine_mfma_kernel",
+            -3: "affine_rows_kernel"}.get(plan[0], "affine_gemv_kernel")
+
+
+def read_floor(gpu: qmr.Gpu, m: synth.PackedMatrix, mats, args) -> dict:
+    """The streaming-read floor of the metric launch: read_checksum (16-byte
+    non-temporal loads over contiguous per-workgroup slices, XOR-reduced into
+    4096 slots) reads the same codes, scales and biases over the same
+    rotating copies, timed the same way as the GEMV. It does no arithmetic
+    beyond the XOR, so its time bounds what any kernel that reads these
+    bytes once can take on this device; the XOR of the slots is checked
+    against the host's XOR of every word."""
+    outs = [gpu.alloc_f32(qmr.CHECKSUM_SLOTS) for _ in mats]
+    bufsets = [[w, s, b, o] for (w, s, b), o in zip(mats, outs)]
+    params = [m.w.nbytes, m.s.nbytes, m.b.nbytes]
+    log(f"bench: read floor, read_checksum of {m.nbytes} bytes ({len(mats)} rotating copies)")
+    mean_ms, _, durs = time_kernel(gpu, "read_checksum", bufsets, params, args.steps, args.warmup)
+    want = np.uint32(0)
+    for a in (m.w, m.s, m.b):
+        want ^= np.bitwise_xor.reduce(np.ascontiguousarray(a).view(np.uint32))
+    got = np.bitwise_xor.reduce(gpu.read_f32(outs[0], qmr.CHECKSUM_SLOTS).view(np.uint32))
+    if got != want:
+        raise RuntimeError(f"read_checksum XOR {got:#x} != host {want:#x}")
+    q = np.quantile(durs, [0.1, 0.5, 0.9])
+    return {"kernel": "read_checksum_kernel", "bytes": int(m.nbytes),
+            "us_mean": round(mean_ms * 1e3, 3),
+            "us_bracketed_p10_p50_p90": [round(v * 1e3, 3) for v in q],
+            "gbps": round(m.nbytes / (mean_ms * 1e-3) / 1e9, 1)}
 
 
 def load_traffic(tag: str):
@@ -512,6 +547,7 @@ def main() -> int:
         shapes.append(("gate_up", synth.MLP_SHAPES["gate_up"]))
     results = []
     metric_matrix = None
+    floor = None
     for tag, (rows, cols) in shapes:
         m = synth.q4_bf16_matrix(rows, cols, synth.DEFAULT_SEED, tag=tag)
         if tag == "down":
@@ -533,6 +569,7 @@ def main() -> int:
                 "shape": f"{rows}x{cols}", "tag": tag, "batch": batch,
                 "reference_pipeline": gpu.last_kernel(),
                 "kernel": hip_kernel(gpu.gemv_plan(rows, cols, 4, batch)),
+                "hip_launch": gpu.last_hip_kernel(),
                 "plan": list(gpu.gemv_plan(rows, cols, 4, batch)),
                 "us_mean": round(mean_ms * 1e3, 3),
                 "us_bracketed_p10_p50_p90": [round(v * 1e3, 3) for v in q],
@@ -546,6 +583,9 @@ def main() -> int:
                 f"{100 * r['frac_peak']:.1f}% of peak")
             results.append(r)
             del bufsets, ys, xb
+        if tag == "down":
+            floor = read_floor(gpu, m, mats, args)
+            log(f"bench:   read floor {floor['us_mean']} us ({floor['gbps']} GB/s)")
         del mats
 
     wide = [] if args.only_metric else bench_wide(gpu, args)
@@ -594,7 +634,15 @@ def main() -> int:
             "frac": head["frac_peak"],
             "traffic": load_traffic("down_b1"),
             "kernel": hip_kernel(head["plan"]),
+            "launch": head["hip_launch"],
+            # The same 50 MB read by read_checksum with the same rotation and
+            # timing; frac_of_floor = floor time / GEMV time.
+            "read_floor_us": floor["us_mean"] if floor else None,
+            "read_floor_gbps": floor["gbps"] if floor else None,
+            "frac_of_floor": round(floor["us_mean"] / head["us_mean"], 4) if floor else None,
+            "frac_of_floor_b3": round(floor["us_mean"] / b3["us_mean"], 4) if floor else None,
         },
+        "read_floor": floor,
         "cpu_baseline": cpu,
         "results": results,
         "config3": config3,

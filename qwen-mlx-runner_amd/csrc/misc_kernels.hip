@@ -253,42 +253,45 @@ __global__ __launch_bounds__(256) void copy_f32_kernel(const float *__restrict__
     for (uint32_t i = nv * 4 + tid; i < n; i += stride) y[i] = x[i];
 }
 
-// Pure streaming read of three views (sizes in bytes, multiples of 4) as
-// workgroup-contiguous slices of 16-byte non-temporal loads, U per thread in
-// flight; slot g receives the XOR of workgroup g's words and workgroup 0
-// zeroes the slots past the grid. The shape measured fastest for one read of
-// ~50 MB on MI355X (back-to-back launches over rotating copies): many small
-// workgroups, each slice requested at once.
+// Pure streaming read of three views (sizes in bytes, multiples of 4). The
+// views' whole 16-byte chunks form one index space, cut into one contiguous
+// slice per workgroup; each thread requests U chunks at once with 16-byte
+// non-temporal loads (a view's chunk run may start at any 4-byte offset), so
+// a workgroup's slice, which may span two views, costs one memory round trip.
+// Slot g receives the XOR of workgroup g's words, the last workgroup also
+// reads the views' trailing (bytes % 16) / 4 words, and workgroup 0 zeroes
+// the slots past the grid. The shape measured fastest for one read of ~50 MB
+// on MI355X (back-to-back launches over rotating copies): ~4096 workgroups
+// of 256 threads, one slice each.
 template <int U>
-__global__ __launch_bounds__(256) void read_checksum_kernel(const void *a, uint32_t na, const void *b, uint32_t nb,
-                                                            const void *c, uint32_t nc, uint32_t *out,
+__global__ __launch_bounds__(256) void read_checksum_kernel(const unsigned char *a, uint32_t na,
+                                                            const unsigned char *b, uint32_t nb,
+                                                            const unsigned char *c, uint32_t nc, uint32_t *out,
                                                             uint32_t slots) {
     const uint32_t G = gridDim.x, g = blockIdx.x, t = threadIdx.x;
-    const void *ptr[3] = {a, b, c};
-    const uint32_t bytes[3] = {na, nb, nc};
+    const uint32_t ca = na / 16, cab = ca + nb / 16, total = cab + nc / 16;
+    const uint32_t per = (total + G - 1) / G;
+    const uint32_t lo = g * per, hi = min(lo + per, total);
     uint32_t acc = 0;
+    for (uint32_t k = lo + t; k < hi; k += 256u * U) {
+        copy_u4 q[U];
 #pragma unroll
-    for (int v = 0; v < 3; ++v) {
-        if (bytes[v] == 0) continue;
-        const __amdgpu_buffer_rsrc_t r =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(ptr[v]), 0, int(bytes[v]), mfma::kRsrcWord3);
-        const uint32_t chunks = bytes[v] / 16;  // whole 16-byte chunks
-        const uint32_t per = (chunks + G - 1) / G;
-        const uint32_t lo = g * per, hi = min(lo + per, chunks);
-        for (uint32_t k = lo + t; k < hi; k += 256u * U) {
-            copy_u4 q[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t kk = k + 256u * u;
-                q[u] = __builtin_amdgcn_raw_buffer_load_b128(r, int(kk < hi ? kk * 16u : mfma::kOut), 0,
-                                                             mfma::kAuxStream);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) acc ^= q[u][0] ^ q[u][1] ^ q[u][2] ^ q[u][3];
+        for (int u = 0; u < U; ++u) {
+            const uint32_t kk = k + 256u * u;
+            const unsigned char *p = kk < ca ? a + size_t(kk) * 16u
+                                   : kk < cab ? b + size_t(kk - ca) * 16u
+                                              : c + size_t(kk - cab) * 16u;
+            q[u] = kk < hi ? __builtin_nontemporal_load(reinterpret_cast<const copy_u4 *>(p)) : copy_u4{0, 0, 0, 0};
         }
-        // The last (bytes % 16) / 4 words, by the last workgroup.
-        if (g == G - 1 && t < (bytes[v] % 16) / 4)
-            acc ^= __builtin_amdgcn_raw_buffer_load_b32(r, int(chunks * 16u + t * 4u), 0, 0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= q[u][0] ^ q[u][1] ^ q[u][2] ^ q[u][3];
+    }
+    // Trailing words: lanes 0-2 of view a, 4-6 of b, 8-10 of c.
+    if (g == G - 1 && t < 12 && (t & 3) < 3) {
+        const uint32_t v = t >> 2, i = t & 3;
+        const uint32_t n = v == 0 ? na : (v == 1 ? nb : nc);
+        const unsigned char *base = v == 0 ? a : (v == 1 ? b : c);
+        if (i < (n % 16) / 4) acc ^= *reinterpret_cast<const uint32_t *>(base + size_t(n / 16) * 16u + i * 4u);
     }
     __shared__ uint32_t red[4];
     for (int m = 32; m >= 1; m >>= 1) acc ^= uint32_t(__shfl_xor(int(acc), m, 64));
@@ -308,8 +311,9 @@ hipError_t launch_read_checksum(const void *a, uint32_t na, const void *b, uint3
     // [256, kChecksumSlots] workgroups.
     uint64_t g = (total + 12287) / 12288;
     g = g < 256 ? 256 : (g > kChecksumSlots ? kChecksumSlots : g);
-    hipLaunchKernelGGL(read_checksum_kernel<4>, dim3(uint32_t(g)), dim3(256), 0, stream, a, na, b, nb, c, nc, out,
-                       kChecksumSlots);
+    hipLaunchKernelGGL(read_checksum_kernel<4>, dim3(uint32_t(g)), dim3(256), 0, stream,
+                       static_cast<const unsigned char *>(a), na, static_cast<const unsigned char *>(b), nb,
+                       static_cast<const unsigned char *>(c), nc, out, kChecksumSlots);
     return hipGetLastError();
 }
 

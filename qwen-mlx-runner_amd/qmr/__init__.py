@@ -30,6 +30,9 @@ QMR_ERR_UNSUPPORTED = 3
 
 BLOCK_MODES = {"legacy": 0, "shared": 1, "mlp-r2": 2}
 BLOCK_MODE_NAMES = {v: k for k, v in BLOCK_MODES.items()}
+# Output slots of the read_checksum kernel (u32; their XOR is the XOR of every
+# word read).
+CHECKSUM_SLOTS = 4096
 
 EXPORTED_SYMBOLS = (
     "qmr_last_error", "qmr_device_open", "qmr_device_close", "qmr_device_name",
