@@ -125,6 +125,22 @@ int qmr_command_begin(qmr_device *device, qmr_command **out);
 int qmr_encode(qmr_command *command, const char *name, qmr_buffer *const *buffers,
                const size_t *offsets, size_t nbuffers, const uint32_t *params,
                size_t nparams, size_t threads, size_t group_size);
+/* No counterpart in the reference: qmr_encode for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc). Same arguments, validation and kernels;
+ * it calls no hipMalloc, hipFree or allocating library routine. The
+ * workspace its kernels need (the row-band kernel's split sums, the split-K
+ * kernel's partial sums and counters, the wide block's activation images)
+ * comes from a static scratch array of QMR_STATIC_SCRATCH_BYTES that each GPU
+ * holds from library load until the process ends; a launch needing more is
+ * rejected with QMR_ERR_INVALID before anything is enqueued. Workspace that
+ * must start at zero is cleared by a fill kernel inside the call. All calls
+ * on one GPU share its scratch: calls whose launches overlap in time (other
+ * streams, other device handles on the same GPU) race. */
+#define QMR_STATIC_SCRATCH_BYTES (8u << 20)
+int qmr_encode_static(qmr_command *command, const char *name, qmr_buffer *const *buffers,
+                      const size_t *offsets, size_t nbuffers, const uint32_t *params,
+                      size_t nparams, size_t threads, size_t group_size);
 /* Records a HIP event on the device stream; *index identifies it for
  * qmr_command_elapsed after the command finishes. (The Metal backend's
  * counterpart is the GPU start/end timestamp pair of FrameTiming.) */

@@ -9,7 +9,8 @@
 //   - copy_f32 (kernels/matmul_block.metal:315-318), a streaming copy that is
 //     also the known-size kernel HBM byte counters are calibrated against;
 //   - read_checksum (no reference counterpart): one pure streaming read of up
-//     to three views, the read floor of a product's codes and metadata.
+//     to three views, the read floor of a product's codes and metadata;
+//   - a zero fill for workspace that must start cleared.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -314,6 +315,20 @@ hipError_t launch_read_checksum(const void *a, uint32_t na, const void *b, uint3
     hipLaunchKernelGGL(read_checksum_kernel<4>, dim3(uint32_t(g)), dim3(256), 0, stream,
                        static_cast<const unsigned char *>(a), na, static_cast<const unsigned char *>(b), nb,
                        static_cast<const unsigned char *>(c), nc, out, kChecksumSlots);
+    return hipGetLastError();
+}
+
+// Zero fill with vector stores (a kernel rather than hipMemsetAsync, so that
+// a command captured into a graph clears the memory on every replay).
+__global__ __launch_bounds__(256) void zero_u32_kernel(uint32_t *__restrict__ p, uint32_t n) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0u;
+}
+
+hipError_t launch_zero_u32(uint32_t *p, uint32_t n, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    const uint32_t want = (n + 255) / 256;
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(want < 1024 ? want : 1024), dim3(256), 0, stream, p, n);
     return hipGetLastError();
 }
 

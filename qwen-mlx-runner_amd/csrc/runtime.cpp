@@ -8,6 +8,7 @@
 #include <atomic>
 #include <chrono>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <unordered_map>
@@ -18,6 +19,15 @@
 #include "kernels.hpp"
 
 using qmr::Error;
+
+// Scratch of the no-allocation entry point (qmr_encode_static): a fixed array
+// in the code object, so that every GPU the library runs on holds its own
+// copy from module load until the process ends. On the host the array's name
+// is not a device address: host code reaches a GPU's copy only through the
+// address hipGetSymbolAddress returns with that GPU current (scratch_address
+// below, kept in qmr_device::scratch). Every qmr_encode_static call on a GPU
+// shares its copy, which keeps the last call's contents.
+static __device__ __align__(256) unsigned char scratch[QMR_STATIC_SCRATCH_BYTES];
 
 struct qmr_device {
     int ordinal = 0;
@@ -56,6 +66,9 @@ struct qmr_device {
     // Workspace of the wide-block kernel: the activation images.
     unsigned char *ws_wide = nullptr;
     size_t ws_wide_bytes = 0;
+    // This GPU's copy of the static scratch (the workspace of
+    // qmr_encode_static, which allocates nothing).
+    unsigned char *scratch = nullptr;
     // Pinned staging ring of qmr::upload_staged (allocated on first use).
     void *pin[2] = {nullptr, nullptr};
     hipEvent_t pin_done[2] = {nullptr, nullptr};
@@ -199,6 +212,31 @@ size_t pipeline_max_threads(const char *label) {
     return 1024;
 }
 
+// The device address of `scratch` on GPU `ordinal`, looked up once per GPU
+// with that GPU current (the caller has made it current) and kept for the
+// process, like the array itself.
+unsigned char *scratch_address(int ordinal) {
+    static std::mutex mu;
+    static std::unordered_map<int, unsigned char *> addresses;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = addresses.find(ordinal);
+    if (it != addresses.end()) return it->second;
+    void *p = nullptr;
+    check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (static scratch)");
+    ensure(p != nullptr, "hipGetSymbolAddress returned no address for the static scratch", QMR_ERR_DEVICE);
+    addresses.emplace(ordinal, static_cast<unsigned char *>(p));
+    return static_cast<unsigned char *>(p);
+}
+
+// qmr_encode_static runs only launches whose workspace fits the static
+// scratch; larger ones are rejected before anything is enqueued.
+void check_static_scratch(size_t need, const char *what) {
+    ensure(need <= QMR_STATIC_SCRATCH_BYTES,
+           std::string("qmr_encode_static: the ") + what + " need " + std::to_string(need) +
+               " bytes of scratch; the static scratch holds " + std::to_string(QMR_STATIC_SCRATCH_BYTES) +
+               " (use qmr_encode, which grows its workspace)");
+}
+
 // Grow the device workspace (synchronising the stream before an old buffer
 // is freed, since queued launches may still use it).
 void ensure_workspace(qmr_device *dev, size_t partial_bytes, size_t counters) {
@@ -272,8 +310,21 @@ qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a) 
 // stream drains, since queued launches may use the old one) and advance the
 // launch epoch. When the epoch wraps, the slots are cleared so that no stale
 // slot can carry the new epoch.
-hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::TilePlan &pl) {
+hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::TilePlan &pl,
+                       unsigned char *fixed) {
     const size_t need = qmr::affine_tile_workspace(pl, a);
+    dev->last_hip = "affine_band_kernel ring=" + std::to_string(pl.ring) + " ns=" + std::to_string(pl.ns) +
+                    " tr=" + std::to_string(pl.tr) + " kw=" + std::to_string(pl.kw);
+    if (fixed) {
+        // The static scratch holds whatever the last call left there: clear
+        // the slots (a fill kernel, so a captured graph clears them on every
+        // replay) and tag this launch's sums with epoch 1, which no cleared
+        // slot carries.
+        check_static_scratch(need, "row-band split sums");
+        const hipError_t e = qmr::launch_zero_u32(reinterpret_cast<uint32_t *>(fixed), uint32_t(need / 4), dev->stream);
+        if (e != hipSuccess) return e;
+        return qmr::launch_affine_tile(a, pl, reinterpret_cast<unsigned long long *>(fixed), 1u, dev->stream);
+    }
     if (need > dev->ws_slots_bytes) {
         check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
         if (dev->ws_slots) hipFree(dev->ws_slots);
@@ -290,9 +341,25 @@ hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::Til
                       "hipMemsetAsync (band workspace)");
         dev->band_epoch = 1;
     }
-    dev->last_hip = "affine_band_kernel ring=" + std::to_string(pl.ring) + " ns=" + std::to_string(pl.ns) +
-                    " tr=" + std::to_string(pl.tr) + " kw=" + std::to_string(pl.kw);
     return qmr::launch_affine_tile(a, pl, dev->ws_slots, dev->band_epoch, dev->stream);
+}
+
+// Launch the split-K kernel with its partial sums and per-band arrival
+// counters: the device's growable workspace, or with `fixed` (qmr_encode_static)
+// the static scratch, whose counters a fill kernel clears first (the kernel
+// needs them zero; partial sums are written before they are read).
+hipError_t launch_split_k(qmr_device *dev, const qmr::AffineArgs &a, const qmr::MfmaPlan &pl,
+                          unsigned char *fixed) {
+    if (!fixed) {
+        ensure_workspace(dev, qmr::affine_mfma_workspace(pl, a), pl.nbands);
+        return qmr::launch_affine_mfma(a, pl, dev->ws_partial, dev->ws_counters, dev->stream);
+    }
+    const size_t part = (qmr::affine_mfma_workspace(pl, a) + 255) / 256 * 256;
+    check_static_scratch(part + size_t(pl.nbands) * sizeof(uint32_t), "split-K partial sums and counters");
+    uint32_t *counters = reinterpret_cast<uint32_t *>(fixed + part);
+    const hipError_t e = qmr::launch_zero_u32(counters, pl.nbands, dev->stream);
+    if (e != hipSuccess) return e;
+    return qmr::launch_affine_mfma(a, pl, reinterpret_cast<float *>(fixed), counters, dev->stream);
 }
 
 // One packed-affine product of at most four RHS: the row-band matrix-core
@@ -303,11 +370,12 @@ hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::Til
 // rr == -1 selects the vector-ALU tilings, rr == -4 the row-band kernel,
 // rr == -3 the row-owning matrix-core kernel, rr == -2 the split-K kernel
 // whatever its shape (with ks > 0 splits, when that count is feasible).
-hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
+// `fixed` (qmr_encode_static) puts every workspace in the static scratch.
+hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a, unsigned char *fixed) {
     qmr::GemvPlan f = dev->forced_plan;
     if ((f.rr == 0 || f.rr == -4) && qmr::affine_tile_supported(a)) {
         const qmr::TilePlan pl = forced_tile_plan(dev, a);
-        if (pl.kw > 0) return launch_band(dev, a, pl);
+        if (pl.kw > 0) return launch_band(dev, a, pl, fixed);
     }
     if (f.rr == -4) f = qmr::GemvPlan{};  // no band plan for this shape: the default chain
     if (f.rr == -3 && qmr::affine_rows_supported(a)) {
@@ -328,9 +396,8 @@ hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a) {
             }
         }
         if (pl.rt > 0) {
-            ensure_workspace(dev, qmr::affine_mfma_workspace(pl, a), pl.nbands);
             dev->last_hip = "affine_mfma_kernel";
-            return qmr::launch_affine_mfma(a, pl, dev->ws_partial, dev->ws_counters, dev->stream);
+            return launch_split_k(dev, a, pl, fixed);
         }
     }
     // The vector-ALU kernels have no fused epilogue.
@@ -388,6 +455,13 @@ int qmr_device_open(int ordinal, const qmr_device_options *options, qmr_device *
         if (e != hipSuccess) {
             delete dev;
             check_hip(e, "hipStreamCreate");
+        }
+        try {
+            dev->scratch = scratch_address(ordinal);
+        } catch (...) {
+            hipStreamDestroy(dev->stream);
+            delete dev;
+            throw;
         }
         *out = dev;
         return QMR_OK;
@@ -660,13 +734,18 @@ void qmr_command_release(qmr_command *command) {
 // (src/gpu.rs:628-848): layout, buffer views, aliasing, mode bans,
 // selection, thread and group checks, then the launch. ----
 
-int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffers,
-               const size_t *offsets, size_t nbuffers, const uint32_t *params, size_t nparams,
-               size_t threads, size_t group_size) {
+// The body of qmr_encode and qmr_encode_static; with no_alloc every launch
+// takes its workspace from the static scratch and nothing is allocated.
+static int encode_command(qmr_command *command, const char *cname, qmr_buffer *const *buffers,
+                          const size_t *offsets, size_t nbuffers, const uint32_t *params, size_t nparams,
+                          size_t threads, size_t group_size, bool no_alloc) {
     return guarded([&]() -> int {
         ensure(command && !command->finished, "qmr_encode: command not open");
         ensure(cname != nullptr, "qmr_encode: null kernel name");
         qmr_device *dev = command->device;
+        unsigned char *fixed = no_alloc ? dev->scratch : nullptr;
+        ensure(!no_alloc || fixed != nullptr, "qmr_encode_static: the device has no static scratch",
+               QMR_ERR_DEVICE);
         const std::string name = cname;
         ensure(params != nullptr || nparams == 0, "qmr_encode: null params");
         const qmr::Layout layout = qmr::dispatch_layout(name, params, nparams);
@@ -803,9 +882,8 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                 const qmr::GemvPlan f = dev->forced_plan;
                 const qmr::MfmaPlan mp = qmr::plan_affine_mfma(a, dev->limits);
                 if (f.rr != -3 && mp.rt > 0) {
-                    ensure_workspace(dev, qmr::affine_mfma_workspace(mp, a), mp.nbands);
                     dev->last_hip = "affine_mfma_kernel (MLP)";
-                    e = qmr::launch_affine_mfma(a, mp, dev->ws_partial, dev->ws_counters, dev->stream);
+                    e = launch_split_k(dev, a, mp, fixed);
                 } else {
                     const qmr::RowsPlan pl =
                         f.rr == -3 && f.ks > 0
@@ -822,7 +900,7 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                 a.y = reinterpret_cast<float *>(ptr(5));
                 ensure(qmr::affine_mfma_supported(a), name + ": no fused kernel for this format",
                        QMR_ERR_UNSUPPORTED);
-                e = launch_product(dev, a);
+                e = launch_product(dev, a, fixed);
             }
         } else {
             qmr::AffineArgs a{};
@@ -843,7 +921,9 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
             // one split-K block of four: batches of up to eight run as blocks.
             if (wide && qmr::wide_mfma_supported(a) && a.batch > 8) {
                 const size_t need = qmr::wide_mfma_workspace(a);
-                if (need > dev->ws_wide_bytes) {
+                unsigned char *images = fixed;
+                if (fixed) check_static_scratch(need, "wide-block activation images");
+                if (!fixed && need > dev->ws_wide_bytes) {
                     check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
                     if (dev->ws_wide) hipFree(dev->ws_wide);
                     dev->ws_wide = nullptr;
@@ -851,8 +931,9 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                     check_hip(hipMalloc(&dev->ws_wide, need), "hipMalloc (wide workspace)");
                     dev->ws_wide_bytes = need;
                 }
+                if (!fixed) images = dev->ws_wide;
                 dev->last_hip = "wide_mfma_kernel";
-                e = qmr::launch_wide_mfma(a, dev->ws_wide, dev->limits, dev->stream);
+                e = qmr::launch_wide_mfma(a, images, dev->limits, dev->stream);
             } else if (wide) {
                 // Wide blocks of up to eight RHS, and those outside the wide
                 // kernel's format, run as successive blocks of up to four RHS.
@@ -861,18 +942,32 @@ int qmr_encode(qmr_command *command, const char *cname, qmr_buffer *const *buffe
                     sub.batch = a.batch - t0 < 4 ? a.batch - t0 : 4;
                     sub.x = a.x + size_t(t0) * a.cols;
                     sub.y = a.y + size_t(t0) * a.rows;
-                    e = launch_product(dev, sub);
+                    e = launch_product(dev, sub, fixed);
                 }
             } else if (dev->reference || !fast_group) {
                 dev->last_hip = "affine_generic_kernel";
                 e = qmr::launch_affine_generic(a, dev->stream);
             } else {
-                e = launch_product(dev, a);
+                e = launch_product(dev, a, fixed);
             }
         }
         check_hip(e, "kernel launch");
         return QMR_OK;
     });
+}
+
+int qmr_encode(qmr_command *command, const char *name, qmr_buffer *const *buffers,
+               const size_t *offsets, size_t nbuffers, const uint32_t *params, size_t nparams,
+               size_t threads, size_t group_size) {
+    return encode_command(command, name, buffers, offsets, nbuffers, params, nparams, threads, group_size,
+                          false);
+}
+
+int qmr_encode_static(qmr_command *command, const char *name, qmr_buffer *const *buffers,
+                      const size_t *offsets, size_t nbuffers, const uint32_t *params, size_t nparams,
+                      size_t threads, size_t group_size) {
+    return encode_command(command, name, buffers, offsets, nbuffers, params, nparams, threads, group_size,
+                          true);
 }
 
 // ---- host-only contract functions ----

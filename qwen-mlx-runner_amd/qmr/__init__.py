@@ -33,6 +33,8 @@ BLOCK_MODE_NAMES = {v: k for k, v in BLOCK_MODES.items()}
 # Output slots of the read_checksum kernel (u32; their XOR is the XOR of every
 # word read).
 CHECKSUM_SLOTS = 4096
+# Bytes of the static scratch behind qmr_encode_static (QMR_STATIC_SCRATCH_BYTES).
+STATIC_SCRATCH_BYTES = 8 << 20
 
 EXPORTED_SYMBOLS = (
     "qmr_last_error", "qmr_device_open", "qmr_device_close", "qmr_device_name",
@@ -40,7 +42,7 @@ EXPORTED_SYMBOLS = (
     "qmr_set_block_kernel_mode", "qmr_compact_metadata", "qmr_record_compacted_metadata",
     "qmr_metadata_stats", "qmr_buffer_alloc", "qmr_buffer_upload", "qmr_buffer_read",
     "qmr_buffer_write", "qmr_buffer_length", "qmr_buffer_retain", "qmr_buffer_release",
-    "qmr_command_begin", "qmr_encode", "qmr_command_mark", "qmr_command_finish",
+    "qmr_command_begin", "qmr_encode", "qmr_encode_static", "qmr_command_mark", "qmr_command_finish",
     "qmr_command_elapsed", "qmr_command_release", "qmr_dispatch_layout",
     "qmr_checked_buffer_range", "qmr_ranges_overlap", "qmr_specialized_matvec",
     "qmr_specialized_matmul", "qmr_parse_block_kernel_mode", "qmr_pack_bf16_exact",
@@ -134,6 +136,7 @@ def lib() -> C.CDLL:
         "qmr_buffer_release": (None, [vp]),
         "qmr_command_begin": (C.c_int, [vp, C.POINTER(vp)]),
         "qmr_encode": (C.c_int, [vp, C.c_char_p, C.POINTER(vp), szp, sz, u32p, sz, sz, sz]),
+        "qmr_encode_static": (C.c_int, [vp, C.c_char_p, C.POINTER(vp), szp, sz, u32p, sz, sz, sz]),
         "qmr_command_mark": (C.c_int, [vp, C.POINTER(C.c_int)]),
         "qmr_command_finish": (C.c_int, [vp, C.POINTER(_Timing)]),
         "qmr_command_elapsed": (C.c_int, [vp, C.c_int, C.c_int, C.POINTER(C.c_double)]),
@@ -288,8 +291,11 @@ class Command:
         self.timing: Optional[FrameTiming] = None
 
     def encode(self, name: str, buffers: Sequence[Buffer], params: Sequence[int],
-               threads: int, group_size: int, offsets: Optional[Sequence[int]] = None) -> None:
-        """DispatchEncoder::encode / encode_offsets (src/gpu.rs:120-141)."""
+               threads: int, group_size: int, offsets: Optional[Sequence[int]] = None,
+               static_scratch: bool = False) -> None:
+        """DispatchEncoder::encode / encode_offsets (src/gpu.rs:120-141).
+        static_scratch=True calls qmr_encode_static instead: the same launch
+        with its workspace in the GPU's static scratch, allocating nothing."""
         n = len(buffers)
         bufs = (C.c_void_p * max(n, 1))(*[b.handle.value for b in buffers])
         offs = None
@@ -297,8 +303,8 @@ class Command:
             if len(offsets) != n:
                 raise QmrError(QMR_ERR_INVALID, f"{name}: offset count must match buffers")
             offs = (C.c_size_t * max(n, 1))(*[int(o) for o in offsets])
-        _check(lib().qmr_encode(self._h, name.encode(), bufs, offs, n, _u32(params), len(params),
-                                threads, group_size))
+        entry = lib().qmr_encode_static if static_scratch else lib().qmr_encode
+        _check(entry(self._h, name.encode(), bufs, offs, n, _u32(params), len(params), threads, group_size))
 
     def mark(self) -> int:
         idx = C.c_int()
