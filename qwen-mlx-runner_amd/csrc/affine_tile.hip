@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
     const int nthr = blockDim.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: entry bounds are scalar
     const int lane = tid & 63;
     const int r = lane & 15;
     const int lg = lane >> 4;
@@ -194,15 +194,23 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const uint32_t piece2 = lo_half ? sp : kp;
     const uint32_t row_bytes = p.cols / 32 * (BITS * 4);
     const uint32_t rowA = tile_row0 + (r & 7), rowB = tile_row0 + 8 + (r & 7);
-    const uint32_t base1 = rowA * row_bytes + 16 * piece1;
-    const uint32_t base2 = rowB * row_bytes + 16 * piece2;
-    const bool okA = rowA < p.rows, okB = rowB < p.rows;
+    // A lane's two pieces at entry 0 are per-lane offsets, kOut for rows past
+    // the matrix; entry E adds E*128 as the wave-uniform soffset. Lanes sent
+    // to kOut read zeros whatever the entry (kOut + E*128 stays below 2^32),
+    // and in-range lanes stay inside their own row: E < E1 <= n_entries, and
+    // in a row's partial last entry the pieces past the row's end go to kOut.
+    // Entries past the wave's range (the ring's tail) read zeros.
+    const uint32_t tail_bytes = row_bytes & 127u;  // bytes of a partial last entry (0: none)
+    const uint32_t vA = rowA < p.rows ? rowA * row_bytes + 16 * piece1 : kOut;
+    const uint32_t vB = rowB < p.rows ? rowB * row_bytes + 16 * piece2 : kOut;
+    const uint32_t vAt = 16 * piece1 < tail_bytes ? vA : kOut;
+    const uint32_t vBt = 16 * piece2 < tail_bytes ? vB : kOut;
     auto issue = [&](u4 (&c)[2], uint32_t E) {
-        const uint32_t eb = E * 128;
-        const uint32_t o1 = (E < E1 && okA && eb + 16 * piece1 < row_bytes) ? base1 + eb : kOut;
-        const uint32_t o2 = (E < E1 && okB && eb + 16 * piece2 < row_bytes) ? base2 + eb : kOut;
-        c[0] = __builtin_amdgcn_raw_buffer_load_b128(wr, int(o1), 0, kAuxStream);
-        c[1] = __builtin_amdgcn_raw_buffer_load_b128(wr, int(o2), 0, kAuxStream);
+        const bool live = E < E1;
+        const bool last = tail_bytes != 0 && E + 1 == p.n_entries;
+        const int so = int(E * 128u);
+        c[0] = __builtin_amdgcn_raw_buffer_load_b128(wr, int(live ? (last ? vAt : vA) : kOut), so, kAuxStream);
+        c[1] = __builtin_amdgcn_raw_buffer_load_b128(wr, int(live ? (last ? vBt : vB) : kOut), so, kAuxStream);
     };
     u4 ring[P][2];
     __builtin_amdgcn_sched_barrier(0);
