@@ -60,8 +60,11 @@ typedef struct {
     int reference;             /* QWEN_METAL_REFERENCE=1: reference arithmetic mode */
 } qmr_device_options;
 
-/* Replaces FrameTiming (src/gpu/timing.rs:8-21). gpu_seconds comes from HIP
- * events recorded on the device stream at command begin and finish. */
+/* Replaces FrameTiming (src/gpu/timing.rs:8-21). gpu_seconds is device time:
+ * from a HIP event recorded on the device stream right before the command's
+ * first launch (after any workspace growth) to one recorded at finish, so
+ * host time before the first encode is not counted (a command that launched
+ * nothing reports about zero). */
 typedef struct {
     double cpu_encode_seconds;
     double cpu_commit_seconds;

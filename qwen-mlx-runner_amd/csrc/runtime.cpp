@@ -69,6 +69,11 @@ struct qmr_device {
     // This GPU's copy of the static scratch (the workspace of
     // qmr_encode_static, which allocates nothing).
     unsigned char *scratch = nullptr;
+    // The open command whose start event is not recorded yet: it is recorded
+    // on the stream just before the command's first launch (after any
+    // workspace growth), so that a frame's GPU time starts when its GPU work
+    // can start, not when the host began encoding.
+    qmr_command *pending = nullptr;
     // Pinned staging ring of qmr::upload_staged (allocated on first use).
     void *pin[2] = {nullptr, nullptr};
     hipEvent_t pin_done[2] = {nullptr, nullptr};
@@ -84,7 +89,10 @@ struct qmr_buffer {
 struct qmr_command {
     qmr_device *device = nullptr;
     std::chrono::steady_clock::time_point started;
-    std::vector<hipEvent_t> marks;  // marks[0] = begin; finish appends the end
+    // marks[0] = GPU start (recorded before the first launch, or at finish
+    // when nothing was launched); finish appends the end.
+    std::vector<hipEvent_t> marks;
+    bool start_recorded = false;
     bool finished = false;
     int end_mark = -1;
 };
@@ -120,6 +128,20 @@ void ensure(bool ok, const std::string &message, int code = QMR_ERR_INVALID) {
 
 void check_hip(hipError_t e, const char *what) {
     if (e != hipSuccess) throw Error{QMR_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e)};
+}
+
+// Records a command's start event on its device's stream (once).
+void record_start(qmr_command *cmd) {
+    if (cmd->start_recorded) return;
+    if (cmd->device->pending == cmd) cmd->device->pending = nullptr;
+    check_hip(hipEventRecord(cmd->marks[0], cmd->device->stream), "hipEventRecord");
+    cmd->start_recorded = true;
+}
+
+// Records the open command's start event if it is still pending: called by
+// every launch path right before its first launch, after workspace growth.
+void start_gpu(qmr_device *dev) {
+    if (dev->pending) record_start(dev->pending);
 }
 
 }  // namespace
@@ -285,22 +307,51 @@ bool rows_preferred(const qmr::MfmaPlan &pl) {
     return pl.rounds > 1 || (pl.ns > 1 && pl.tps < 4);
 }
 
+// The reference's block schedules (src/gpu.rs:22-31) keep each output row's
+// accumulation order and change only the thread geometry
+// (kernels/matmul_block.metal:291-299). On the row-band kernel the same holds
+// for the ring depth and the row tiles per band, which leave a row's sums
+// untouched, so the schedules the reference routes to its shared and R2
+// pipelines run their own instances: the other ring depth (shared) or half
+// (else twice) the row tiles per band (R2), with the splits and waves of the
+// legacy plan, and produce its bits.
+enum class BandSchedule { Legacy = 0, Shared = 1, R2 = 2 };
+
+BandSchedule band_schedule(const qmr_device *dev) {
+    const std::string &label = dev->last_kernel;
+    if (qmr::ends_with(label, "_mlp_r2_aligned_bf16")) return BandSchedule::R2;
+    if (label.find("_shared_aligned") != std::string::npos) return BandSchedule::Shared;
+    return BandSchedule::Legacy;
+}
+
 // The row-band kernel's plan, honouring a forced shape (rr == -4, ks =
 // ring*100000 + ns*10000 + tr*100 + kw; zero fields leave them to its
-// planner).
-qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a) {
+// planner) and the block schedule; a schedule's instance that has no
+// one-round plan runs the legacy plan.
+qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a,
+                               BandSchedule sched = BandSchedule::Legacy) {
     const qmr::GemvPlan f = dev->forced_plan;
     const int ks = f.rr == -4 ? f.ks : 0;
     uint64_t key = (uint64_t(a.rows) << 32) | a.cols;
     key = key * 1000003u ^ (uint64_t(a.bits) << 24 | uint64_t(a.group) << 12 | uint64_t(a.batch) << 4 |
                             uint64_t(static_cast<int>(a.meta)) << 1 | (a.residual ? 1u : 0u));
     key = key * 1000003u ^ uint64_t(uint32_t(ks));
+    key = key * 1000003u ^ uint64_t(static_cast<int>(sched));
     const auto it = dev->band_plans.find(key);
     if (it != dev->band_plans.end()) return it->second;
-    const qmr::TilePlan pl =
-        ks > 0 ? qmr::plan_affine_tile(a, dev->limits, uint32_t(ks % 100), uint32_t(ks / 100 % 100),
-                                       uint32_t(ks / 10000 % 10), uint32_t(ks / 100000))
-               : qmr::plan_affine_tile(a, dev->limits);
+    qmr::TilePlan pl = sched != BandSchedule::Legacy ? forced_tile_plan(dev, a)
+                       : ks > 0 ? qmr::plan_affine_tile(a, dev->limits, uint32_t(ks % 100), uint32_t(ks / 100 % 100),
+                                                        uint32_t(ks / 10000 % 10), uint32_t(ks / 100000))
+                                : qmr::plan_affine_tile(a, dev->limits);
+    if (pl.kw > 0 && sched == BandSchedule::Shared) {
+        const qmr::TilePlan alt = qmr::plan_affine_tile(a, dev->limits, pl.kw, pl.tr, pl.ns, pl.ring == 4 ? 2 : 4);
+        if (alt.kw > 0) pl = alt;
+    } else if (pl.kw > 0 && sched == BandSchedule::R2) {
+        qmr::TilePlan alt;
+        if (pl.tr >= 2) alt = qmr::plan_affine_tile(a, dev->limits, pl.kw, pl.tr / 2, pl.ns, pl.ring);
+        if (alt.kw == 0 && pl.tr <= 4) alt = qmr::plan_affine_tile(a, dev->limits, pl.kw, pl.tr * 2, pl.ns, pl.ring);
+        if (alt.kw > 0) pl = alt;
+    }
     if (dev->band_plans.size() > 4096) dev->band_plans.clear();
     dev->band_plans.emplace(key, pl);
     return pl;
@@ -321,6 +372,7 @@ hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::Til
         // replay) and tag this launch's sums with epoch 1, which no cleared
         // slot carries.
         check_static_scratch(need, "row-band split sums");
+        start_gpu(dev);
         const hipError_t e = qmr::launch_zero_u32(reinterpret_cast<uint32_t *>(fixed), uint32_t(need / 4), dev->stream);
         if (e != hipSuccess) return e;
         return qmr::launch_affine_tile(a, pl, reinterpret_cast<unsigned long long *>(fixed), 1u, dev->stream);
@@ -341,6 +393,7 @@ hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::Til
                       "hipMemsetAsync (band workspace)");
         dev->band_epoch = 1;
     }
+    start_gpu(dev);
     return qmr::launch_affine_tile(a, pl, dev->ws_slots, dev->band_epoch, dev->stream);
 }
 
@@ -352,11 +405,13 @@ hipError_t launch_split_k(qmr_device *dev, const qmr::AffineArgs &a, const qmr::
                           unsigned char *fixed) {
     if (!fixed) {
         ensure_workspace(dev, qmr::affine_mfma_workspace(pl, a), pl.nbands);
+        start_gpu(dev);
         return qmr::launch_affine_mfma(a, pl, dev->ws_partial, dev->ws_counters, dev->stream);
     }
     const size_t part = (qmr::affine_mfma_workspace(pl, a) + 255) / 256 * 256;
     check_static_scratch(part + size_t(pl.nbands) * sizeof(uint32_t), "split-K partial sums and counters");
     uint32_t *counters = reinterpret_cast<uint32_t *>(fixed + part);
+    start_gpu(dev);
     const hipError_t e = qmr::launch_zero_u32(counters, pl.nbands, dev->stream);
     if (e != hipSuccess) return e;
     return qmr::launch_affine_mfma(a, pl, reinterpret_cast<float *>(fixed), counters, dev->stream);
@@ -374,7 +429,7 @@ hipError_t launch_split_k(qmr_device *dev, const qmr::AffineArgs &a, const qmr::
 hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a, unsigned char *fixed) {
     qmr::GemvPlan f = dev->forced_plan;
     if ((f.rr == 0 || f.rr == -4) && qmr::affine_tile_supported(a)) {
-        const qmr::TilePlan pl = forced_tile_plan(dev, a);
+        const qmr::TilePlan pl = forced_tile_plan(dev, a, band_schedule(dev));
         if (pl.kw > 0) return launch_band(dev, a, pl, fixed);
     }
     if (f.rr == -4) f = qmr::GemvPlan{};  // no band plan for this shape: the default chain
@@ -382,6 +437,7 @@ hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a, unsigned ch
         const qmr::RowsPlan pl = forced_rows_plan(dev, a);
         if (pl.rt > 0) {
             dev->last_hip = "affine_rows_kernel";
+            start_gpu(dev);
             return qmr::launch_affine_rows(a, pl, dev->stream);
         }
     }
@@ -392,6 +448,7 @@ hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a, unsigned ch
             const qmr::RowsPlan rp = qmr::plan_affine_rows(a, dev->limits);
             if (rp.rt > 0) {
                 dev->last_hip = "affine_rows_kernel";
+                start_gpu(dev);
                 return qmr::launch_affine_rows(a, rp, dev->stream);
             }
         }
@@ -403,6 +460,7 @@ hipError_t launch_product(qmr_device *dev, const qmr::AffineArgs &a, unsigned ch
     // The vector-ALU kernels have no fused epilogue.
     ensure(a.residual == nullptr, "fused product needs a matrix-core kernel", QMR_ERR_UNSUPPORTED);
     dev->last_hip = "affine_gemv_kernel";
+    start_gpu(dev);
     return qmr::launch_affine_gemv(a, f.rr < -1 ? qmr::GemvPlan{} : f, dev->limits, dev->stream);
 }
 
@@ -647,13 +705,16 @@ int qmr_command_begin(qmr_device *device, qmr_command **out) {
         cmd->device = device;
         cmd->started = std::chrono::steady_clock::now();
         hipEvent_t ev;
-        hipError_t e = hipEventCreate(&ev);
-        if (e == hipSuccess) e = hipEventRecord(ev, device->stream);
+        const hipError_t e = hipEventCreate(&ev);
         if (e != hipSuccess) {
             delete cmd;
-            check_hip(e, "hipEventRecord");
+            check_hip(e, "hipEventCreate");
         }
         cmd->marks.push_back(ev);
+        // A command opened before this one that has launched nothing starts
+        // here; this one starts at its first launch.
+        if (device->pending) record_start(device->pending);
+        device->pending = cmd;
         *out = cmd;
         return QMR_OK;
     });
@@ -681,6 +742,7 @@ int qmr_command_finish(qmr_command *command, qmr_frame_timing *timing) {
         using clock = std::chrono::steady_clock;
         const double encode = std::chrono::duration<double>(clock::now() - command->started).count();
         const auto commit_start = clock::now();
+        record_start(command);  // a command that launched nothing: zero GPU time
         hipEvent_t end;
         check_hip(hipEventCreate(&end), "hipEventCreate");
         hipError_t e = hipEventRecord(end, command->device->stream);
@@ -725,6 +787,7 @@ int qmr_command_elapsed(const qmr_command *command, int from, int to, double *ms
 
 void qmr_command_release(qmr_command *command) {
     if (!command) return;
+    if (command->device->pending == command) command->device->pending = nullptr;
     if (!command->finished) hipStreamSynchronize(command->device->stream);
     for (hipEvent_t ev : command->marks) hipEventDestroy(ev);
     delete command;
@@ -832,6 +895,9 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
             return static_cast<char *>(buffers[i]->ptr) + off(i);
         };
         hipError_t e = hipSuccess;
+        // Families that launch without workspace start the frame's GPU time
+        // here; the others start it after their workspace is in place.
+        if (!qmr::starts_with(name, "mat") && !fused) start_gpu(dev);
         if (qmr::starts_with(name, "embed_affine")) {
             e = qmr::launch_embed_affine(reinterpret_cast<const uint32_t *>(ptr(0)), ptr(1), ptr(2),
                                          meta, params[0], params[1], params[2], params[3],
@@ -847,6 +913,7 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
             e = qmr::launch_embed_f16(reinterpret_cast<const uint16_t *>(ptr(0)), params[0],
                                       params[1], reinterpret_cast<float *>(ptr(1)), dev->stream);
         } else if (name == "matvec_f16" || name == "matmul_f16") {
+            start_gpu(dev);
             const uint32_t batch = name == "matmul_f16" ? params[2] : 1;
             e = qmr::launch_dense_f16(reinterpret_cast<const uint16_t *>(ptr(0)),
                                       reinterpret_cast<const float *>(ptr(1)),
@@ -892,6 +959,7 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
                             : qmr::plan_affine_mlp(a, dev->limits);
                     ensure(pl.rt > 0, name + ": no fused tiling for this shape", QMR_ERR_UNSUPPORTED);
                     dev->last_hip = "affine_rows_kernel (MLP)";
+                    start_gpu(dev);
                     e = qmr::launch_affine_rows(a, pl, dev->stream);
                 }
             } else {
@@ -933,6 +1001,7 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
                 }
                 if (!fixed) images = dev->ws_wide;
                 dev->last_hip = "wide_mfma_kernel";
+                start_gpu(dev);
                 e = qmr::launch_wide_mfma(a, images, dev->limits, dev->stream);
             } else if (wide) {
                 // Wide blocks of up to eight RHS, and those outside the wide
@@ -946,6 +1015,7 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
                 }
             } else if (dev->reference || !fast_group) {
                 dev->last_hip = "affine_generic_kernel";
+                start_gpu(dev);
                 e = qmr::launch_affine_generic(a, dev->stream);
             } else {
                 e = launch_product(dev, a, fixed);

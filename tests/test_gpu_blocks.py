@@ -198,23 +198,38 @@ def test_selective_mlp_r2_real_shapes_match_legacy_bits_and_fp64_with_guards(gpu
                                                        np.frombuffer(a.tobytes(), np.uint8),
                                                        np.full(16, 0xA5, np.uint8)]))
     wb, sb, bb, xb = guard(w), guard(s16), guard(b16), guard(x)
-    outs = []
+    outs, kernels = [], []
+    labels = {"legacy": "matmul_q4_g64_b3_aligned_bf16", "mlp-r2": "matmul_q4_g64_b3_mlp_r2_aligned_bf16",
+              "shared": "matmul_q4_g64_b3_shared_aligned_bf16"}
     try:
-        for mode in ("legacy", "mlp-r2"):
+        for mode in ("legacy", "mlp-r2", "shared"):
             gpu.set_block_kernel_mode(mode, True)
             y = gpu.upload_f32(np.full(rows * 3 + 8, 12345.0))
             gpu.dispatch("matmul_affine_bf16", [wb, sb, bb, xb, y], [rows, cols, 4, 64, 3],
                          offsets=[16] * 5)
-            label = gpu.last_kernel()
-            assert label == ("matmul_q4_g64_b3_mlp_r2_aligned_bf16" if mode == "mlp-r2"
-                             else "matmul_q4_g64_b3_aligned_bf16")
+            assert gpu.last_kernel() == labels[mode]
+            kernels.append(gpu.last_hip_kernel())
             outs.append(gpu.read_f32(y, rows * 3 + 8))
     finally:
         gpu.set_block_kernel_mode("legacy", True)
+    # The schedules run their own instances of the row-band kernel with the
+    # legacy splits and waves, so every row's sums are the same operations:
+    # shared takes the other ring depth; R2 halves (else doubles) the row
+    # tiles per band where that shape has a one-round plan, which at
+    # 5120x17408 B=3 neither has (its x images leave one workgroup per CU,
+    # and eight tiles of two waves exceed 512 threads), so there R2 runs the
+    # legacy instance.
+    assert all(k.startswith("affine_band_kernel") for k in kernels), kernels
+    assert kernels[2] != kernels[0], kernels
+    if (rows, cols) == (17408, 5120):
+        assert len(set(kernels)) == 3, kernels
+    else:
+        assert kernels[1] == kernels[0], kernels
     for got in outs:
         assert (got[:4] == 12345.0).all() and (got[rows * 3 + 4:] == 12345.0).all()
         assert np.isfinite(got[4:rows * 3 + 4]).all()
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
     sample = [k * (rows - 1) // 31 for k in range(32)]
     sub = lambda a, per: np.concatenate([a[r * per:(r + 1) * per] for r in sample])
     want = oracle.matmul_f64(sub(w, cols // 8), sub(s16, cols // 64), sub(b16, cols // 64), "bf16",

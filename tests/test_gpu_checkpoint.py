@@ -54,7 +54,8 @@ def test_fixture_matrices_load_and_multiply(tmp_path, tag, mode):
     """All 33 fixture matrices: the device holds the checkpoint's words
     unchanged and its metadata as BF16 exactly when the device's metadata
     mode is "bf16" and the values compact losslessly (the BF16 checkpoint
-    always does); B=1 and B=3 products meet the gate."""
+    always does, and the device's metadata_stats then report the reference's
+    (33, 6576)); B=1 and B=3 products meet the gate."""
     names = _fixture_checkpoint(tmp_path, tag)
     gpu = qmr.Gpu("aligned", metadata=mode)
     try:
@@ -80,6 +81,10 @@ def test_fixture_matrices_load_and_multiply(tmp_path, tag, mode):
                     assert_gate(_product(gpu, m, x, batch), want, f"{name} {mode} B{batch}")
         if mode == "f32":
             assert gpu.metadata_stats()[0] == 0
+        if (tag, mode) == ("q4bf16", "bf16"):
+            # tests/bf16_inference.rs:11-15: every tiny-bf16 matrix compacted,
+            # 3288 scales and biases kept at 2 bytes instead of 4.
+            assert gpu.metadata_stats() == (33, 3288 * 2)
     finally:
         gpu.close()
 

@@ -341,3 +341,95 @@ def test_read_checksum_reads_every_word_once(gpu, sizes, offsets):
             if v.size:
                 want ^= np.bitwise_xor.reduce(v)
         assert np.bitwise_xor.reduce(slots) == want, f"launch {launch}"
+
+
+def test_frame_gpu_seconds_is_device_time(gpu):
+    """FrameTiming.gpu_seconds (src/gpu/timing.rs:8-21; the Metal command
+    buffer's GPU start/end) covers the command's GPU work only: the start
+    event is recorded right before the first launch, so host time spent
+    between begin and the first encode is not counted. A wide block (two
+    launches, ~0.1 ms) encoded after 50 ms of host sleep: gpu_seconds is at
+    most the command's wall time and within 1.5x of the elapsed time between
+    marks around the encode."""
+    import time
+    rng = np.random.default_rng(3)
+    rows, cols, batch = 17408, 5120, 256
+    w = rng.integers(0, 2**32, rows * cols // 8, dtype=np.uint64).astype(np.uint32)
+    s = synth.f32_to_bf16_bits(rng.uniform(0.002, 0.02, rows * cols // 64).astype(np.float32))
+    b = synth.f32_to_bf16_bits(rng.uniform(-0.1, 0.0, rows * cols // 64).astype(np.float32))
+    x = rng.normal(0, 1, batch * cols).astype(np.float32)
+    bufs = [gpu.upload_bytes(w), gpu.upload_bytes(s), gpu.upload_bytes(b), gpu.upload_f32(x),
+            gpu.alloc_f32(batch * rows)]
+    name, params = "matmul_affine_wide_bf16", [rows, cols, 4, 64, batch]
+    _, threads = qmr.dispatch_layout(name, params)
+    gpu.dispatch(name, bufs, params)  # workspace growth happens here, outside the timed command
+    for _ in range(3):
+        t0 = time.perf_counter()
+        cmd = gpu.begin()
+        time.sleep(0.05)
+        a = cmd.mark()
+        cmd.encode(name, bufs, params, threads, 128)
+        c = cmd.mark()
+        timing = cmd.finish()
+        wall = time.perf_counter() - t0
+        around = cmd.elapsed_ms(a, c) * 1e-3
+        cmd.release()
+        assert 0.0 < timing.gpu_seconds <= wall, (timing.gpu_seconds, wall)
+        assert around / 1.5 <= timing.gpu_seconds <= around * 1.5, (timing.gpu_seconds, around)
+    # A warm config-0 command (1024x1024 GEMV, a few microseconds): the marks
+    # around it also hold the host's encode time, which the GPU time
+    # excludes, so here only the upper bounds apply.
+    m = synth.q4_bf16_matrix(1024, 1024, 1, tag="config0")
+    x0 = synth.activations(1024, 1, 1, tag="config0")
+    bufs0 = [gpu.upload_bytes(m.w), gpu.upload_bytes(m.s), gpu.upload_bytes(m.b), gpu.upload_f32(x0),
+             gpu.alloc_f32(1024)]
+    gpu.dispatch("matvec_affine_bf16", bufs0, [1024, 1024, 4, 64])
+    for _ in range(3):
+        t0 = time.perf_counter()
+        cmd = gpu.begin()
+        time.sleep(0.05)
+        a = cmd.mark()
+        cmd.encode("matvec_affine_bf16", bufs0, [1024, 1024, 4, 64], 1024 * 32, 128)
+        c = cmd.mark()
+        timing = cmd.finish()
+        wall = time.perf_counter() - t0
+        around = cmd.elapsed_ms(a, c) * 1e-3
+        cmd.release()
+        assert 0.0 < timing.gpu_seconds <= min(wall, around * 1.5), (timing.gpu_seconds, wall, around)
+
+
+@pytest.mark.parametrize("name,bits,group", [("embed_affine", 4, 64), ("embed_affine", 8, 32),
+                                             ("embed_affine_bf16", 4, 64), ("embed_affine_bf16", 8, 128),
+                                             ("embed_f16", 0, 0)])
+def test_embed_offset_writes_only_its_slot_bit_exact(gpu, name, bits, group):
+    """Matrix::embed_offset (src/engine/block.rs:231-261): encode_offsets
+    with the output view at byte offset slot*cols*4 of a [batch][cols]
+    buffer, as the block path embeds token i into row i
+    (src/engine/block.rs:426). The row lands bit-exact (RN32(q*s + b), or the
+    F16 row widened) in its slot; every word before and after it keeps its
+    guard value."""
+    rng = np.random.default_rng([bits, group, len(name)])
+    rows, cols, batch, slot, token = 9, 1024, 4, 2, 5
+    guard = np.uint32(0x7FC0DEAD)  # a quiet NaN pattern no dequantised value has
+    ybuf = gpu.upload_bytes(np.full(batch * cols, guard, np.uint32))
+    if name == "embed_f16":
+        dense = rng.normal(0, 1, rows * cols).astype(np.float16)
+        bufs = [gpu.upload_bytes(dense.view(np.uint16))]
+        params = [token, cols]
+        want = dense.reshape(rows, cols)[token].astype(np.float32)
+    else:
+        w = rng.integers(0, 2**32, rows * cols * bits // 32, dtype=np.uint64).astype(np.uint32)
+        s = rng.uniform(0.002, 0.02, rows * cols // group).astype(np.float32)
+        b = rng.uniform(-0.2, 0.0, rows * cols // group).astype(np.float32)
+        kind = "f32"
+        if name.endswith("_bf16"):
+            s, b, kind = synth.f32_to_bf16_bits(s), synth.f32_to_bf16_bits(b), "bf16"
+        bufs = [gpu.upload_bytes(w), gpu.upload_bytes(s), gpu.upload_bytes(b)]
+        params = [token, cols, bits, group]
+        want = oracle.dequant_row(w, s, b, kind, token, cols, bits, group)
+    offsets = [0] * len(bufs) + [slot * cols * 4]
+    gpu.dispatch(name, bufs + [ybuf], params, offsets=offsets)
+    got = np.frombuffer(ybuf.read_bytes(0, batch * cols * 4), np.uint32).reshape(batch, cols)
+    assert np.array_equal(got[slot], want.view(np.uint32)), name
+    others = np.delete(got, slot, axis=0)
+    assert np.all(others == guard), name
