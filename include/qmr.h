@@ -247,6 +247,15 @@ const char *qmr_last_kernel(const qmr_device *device);
 const char *qmr_last_hip_kernel(const qmr_device *device);
 /* LDS bytes one workgroup may allocate on this device. */
 size_t qmr_device_max_lds(const qmr_device *device);
+/* Host-only check of the wide block kernel's addressing (no device needed):
+ * walks every code, x-fragment and group-sum load its contraction launch
+ * issues for rows x cols (a multiple of 256) times batch RHS with row_tiles
+ * (8 or 17) 16-row tiles per workgroup, and writes out[0] = the largest end
+ * (byte offset + size) of the in-range code loads, out[1] = the code view's
+ * size, out[2] = the largest end of the in-range image loads, out[3] = the
+ * image workspace's size. Loads outside a view take the vector offset past
+ * every view and read zeros. */
+int qmr_wide_address_extent(uint32_t rows, uint32_t cols, uint32_t batch, uint32_t row_tiles, uint64_t *out);
 
 #ifdef __cplusplus
 }

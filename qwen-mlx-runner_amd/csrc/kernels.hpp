@@ -154,6 +154,14 @@ bool wide_mfma_supported(const AffineArgs &a);
 size_t wide_mfma_workspace(const AffineArgs &a);
 hipError_t launch_wide_mfma(const AffineArgs &a, unsigned char *workspace, const DeviceLimits &lim,
                             hipStream_t stream);
+// Host-side walk of every code, x-fragment and group-sum load the wide
+// contraction kernel issues for a shape with nrt row tiles per block: the
+// largest end (offset + size) of the in-range loads in the code view and in
+// the image workspace, beside the two extents.
+struct WideExtent {
+    uint64_t code_end, code_extent, image_end, image_extent;
+};
+WideExtent wide_address_extent(uint32_t rows, uint32_t cols, uint32_t n, uint32_t nrt);
 
 // The plan the GEMV launcher would use (for tests and tuning reports).
 GemvPlan plan_affine_gemv(const AffineArgs &a, GemvPlan forced, const DeviceLimits &lim);

@@ -1026,6 +1026,21 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
     });
 }
 
+int qmr_wide_address_extent(uint32_t rows, uint32_t cols, uint32_t batch, uint32_t row_tiles, uint64_t *out) {
+    return guarded([&]() -> int {
+        ensure(out != nullptr, "qmr_wide_address_extent: null output");
+        ensure(rows > 0 && cols > 0 && cols % 256 == 0 && batch >= 1 && batch <= 256 &&
+                   (row_tiles == 8 || row_tiles == 17) && uint64_t(rows) * cols / 2 < (1ull << 31),
+               "qmr_wide_address_extent: unsupported shape");
+        const qmr::WideExtent e = qmr::wide_address_extent(rows, cols, batch, row_tiles);
+        out[0] = e.code_end;
+        out[1] = e.code_extent;
+        out[2] = e.image_end;
+        out[3] = e.image_extent;
+        return QMR_OK;
+    });
+}
+
 int qmr_encode(qmr_command *command, const char *name, qmr_buffer *const *buffers,
                const size_t *offsets, size_t nbuffers, const uint32_t *params, size_t nparams,
                size_t threads, size_t group_size) {

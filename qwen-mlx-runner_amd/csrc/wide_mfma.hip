@@ -75,6 +75,38 @@ constexpr size_t wide_lds_bytes(int nrt) {
     return meta > red ? meta : red;
 }
 
+// Byte offsets of the contraction kernel's code, x-fragment and group-sum
+// loads, as the per-lane vector offset and the wave-uniform scalar offset of
+// a buffer load. A load outside its view (a row past the matrix, a group
+// past the row, an image past the last group) gets the vector offset kOut,
+// which by itself lies past every view's extent, so it reads zeros whether
+// or not the range check adds the scalar offset (kOut plus any scalar offset
+// here stays below 2^32); every other load has voffset + soffset + size
+// within its view. qmr_wide_address_extent walks every load the kernel can
+// issue through these functions on the host.
+struct WideAddr {
+    uint32_t rows, G, ntb, row_bytes;
+    // The 8-byte code piece of lane (r16, q) in row tile rt of the row block
+    // at row0, quant group g (lanes q hold the group's four 16-column quarters).
+    __host__ __device__ uint32_t code_v(uint32_t row0, uint32_t rt, uint32_t r16, uint32_t q, uint32_t g) const {
+        return (row0 + 16 * rt + r16 < rows && g < G) ? (row0 + r16) * row_bytes + q * 8 : kOut;
+    }
+    __host__ __device__ uint32_t code_s(uint32_t rt, uint32_t g) const { return rt * 16 * row_bytes + g * 32; }
+    // Fragment f of group g's image for RHS block tb; lane l reads 16 bytes.
+    __host__ __device__ uint32_t frag_v(uint32_t lane, uint32_t g) const { return g < G ? lane * 16 : kOut; }
+    __host__ __device__ uint32_t frag_s(uint32_t g, uint32_t tb, uint32_t f) const {
+        return (g * ntb + tb) * uint32_t(kImgBytes) + f * uint32_t(kFragBytes);
+    }
+    // Group sum of RHS 16 ct + r16 in block tb for group g0 + 4 q (lane
+    // (r16, q)); g0 = 16 c + class.
+    __host__ __device__ uint32_t sum_v(uint32_t g0, uint32_t q, uint32_t r16, uint32_t ct) const {
+        return g0 + 4 * q < G ? q * 4 * ntb * uint32_t(kImgBytes) + uint32_t(kImgS) + r16 * 4 + ct * 64 : kOut;
+    }
+    __host__ __device__ uint32_t sum_s(uint32_t g0, uint32_t tb) const {
+        return (g0 * ntb + tb) * uint32_t(kImgBytes);
+    }
+};
+
 struct WideParams {
     const uint32_t *w;
     const void *s;
@@ -173,6 +205,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
     const uint32_t G = p.cols / 64;
     const uint32_t nch = (G + kCG - 1) / kCG;
     const uint32_t row_bytes = p.cols / 2;
+    const WideAddr A{p.rows, G, p.ntb, row_bytes};
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t *>(p.w), 0, int(p.w_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t ir = __builtin_amdgcn_make_buffer_rsrc(
@@ -249,33 +282,30 @@ __global__ __launch_bounds__(kThreads, 1) void wide_mfma_kernel(WideParams p) {
     {
         constexpr int NTW = NRT;
         // Code piece of row tile rt: words 2q, 2q+1 of the group for row
-        // row0 + 16 rt + r16. The row tile and group move only the
-        // scalar offset; the buffer range check covers vector plus scalar
-        // offset, so rows past the matrix read zeros (and groups past the
-        // row read the next row's codes, which meet zero scales).
-        const uint32_t cbase = (row0 + uint32_t(r16)) * row_bytes + uint32_t(q) * 8;
-        const uint32_t cstride = 16 * row_bytes;
+        // row0 + 16 rt + r16 (WideAddr: rows past the matrix and groups past
+        // the row read zeros through the vector offset).
         u2 cw[NTW];
         auto load_codes = [&](int rt, uint32_t g) {
-            cw[rt] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                 wr, int(cbase), int(uint32_t(rt) * cstride + g * 32), 0));
+            cw[rt] = __builtin_bit_cast(
+                u2, __builtin_amdgcn_raw_buffer_load_b64(wr, int(A.code_v(row0, uint32_t(rt), uint32_t(r16), uint32_t(q), g)),
+                                                         int(A.code_s(uint32_t(rt), g)), 0));
         };
         // x fragments of group g: f = (ks*2 + ct)*2 + hl, lane i at 16 i
-        // (past the last group: past the images, zeros).
-        const uint32_t xo = uint32_t(lane) * 16;
+        // (past the last group: zeros).
         auto load_x = [&](h8 (&xf)[8], uint32_t g) {
-            const int base = int((g * p.ntb + tb) * kImgBytes);
+            const int xo = int(A.frag_v(uint32_t(lane), g));
 #pragma unroll
             for (int f = 0; f < 8; ++f)
-                xf[f] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(ir, int(xo), base + f * kFragBytes, 0));
+                xf[f] = __builtin_bit_cast(
+                    h8, __builtin_amdgcn_raw_buffer_load_b128(ir, xo, int(A.frag_s(g, tb, uint32_t(f))), 0));
         };
         // Bias A operands of chunk c: S[16c + 4q + kr][16 ct + r16].
-        const uint32_t so = uint32_t(q) * 4 * p.ntb * kImgBytes + kImgS + uint32_t(r16) * 4;
         auto load_s = [&](float (&sop)[2], uint32_t c) {
-            const int base = int(((c * kCG + uint32_t(kr)) * p.ntb + tb) * kImgBytes);
+            const uint32_t g0 = c * kCG + uint32_t(kr);
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct)
-                sop[ct] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ir, int(so + ct * 64), base, 0));
+                sop[ct] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    ir, int(A.sum_v(g0, uint32_t(q), uint32_t(r16), uint32_t(ct))), int(A.sum_s(g0, tb)), 0));
         };
 
         f4 acc[NTW][2];
@@ -492,6 +522,39 @@ bool wide_mfma_supported(const AffineArgs &a) {
 size_t wide_mfma_workspace(const AffineArgs &a) {
     const size_t ntb = (a.batch + kRhsBlock - 1) / kRhsBlock;
     return size_t(a.cols / 64) * ntb * kImgBytes;
+}
+
+WideExtent wide_address_extent(uint32_t rows, uint32_t cols, uint32_t n, uint32_t nrt) {
+    WideExtent out{};
+    const uint32_t G = cols / 64, nch = (G + kCG - 1) / kCG, ntb = (n + kRhsBlock - 1) / kRhsBlock;
+    const uint32_t nrb = (rows + 16 * nrt - 1) / (16 * nrt);
+    const WideAddr A{rows, G, ntb, cols / 2};
+    out.code_extent = uint64_t(rows) * cols / 2;
+    out.image_extent = uint64_t(G) * ntb * kImgBytes;
+    auto note = [](uint64_t &mx, uint32_t v, uint32_t so, uint32_t size) {
+        if (v != kOut) mx = std::max(mx, uint64_t(v) + so + size);
+    };
+    // Groups the kernel requests per class kr: the first (kr) and, for each
+    // group it processes (16c + kr + 4i, c < nch, i < 4), the one four
+    // groups on (codes and x fragments alike); group sums per chunk c <= nch.
+    for (uint32_t kr = 0; kr < uint32_t(kKRanges); ++kr) {
+        for (uint32_t j = 0; j <= 4 * nch; ++j) {
+            const uint32_t g = kr + 4 * j;
+            for (uint32_t rb = 0; rb < nrb; ++rb)
+                for (uint32_t rt = 0; rt < nrt; ++rt)
+                    for (uint32_t l = 0; l < 64; ++l)
+                        note(out.code_end, A.code_v(rb * 16 * nrt, rt, l & 15, l >> 4, g), A.code_s(rt, g), 8);
+            for (uint32_t tb = 0; tb < ntb; ++tb)
+                for (uint32_t f = 0; f < 8; ++f)
+                    for (uint32_t l = 0; l < 64; ++l) note(out.image_end, A.frag_v(l, g), A.frag_s(g, tb, f), 16);
+        }
+        for (uint32_t c = 0; c <= nch; ++c)
+            for (uint32_t tb = 0; tb < ntb; ++tb)
+                for (uint32_t l = 0; l < 64; ++l)
+                    for (uint32_t ct = 0; ct < 2; ++ct)
+                        note(out.image_end, A.sum_v(c * kCG + kr, l >> 4, l & 15, ct), A.sum_s(c * kCG + kr, tb), 4);
+    }
+    return out;
 }
 
 hipError_t launch_wide_mfma(const AffineArgs &a, unsigned char *workspace, const DeviceLimits &lim,

@@ -46,7 +46,7 @@ EXPORTED_SYMBOLS = (
     "qmr_command_elapsed", "qmr_command_release", "qmr_dispatch_layout",
     "qmr_checked_buffer_range", "qmr_ranges_overlap", "qmr_specialized_matvec",
     "qmr_specialized_matmul", "qmr_parse_block_kernel_mode", "qmr_pack_bf16_exact",
-    "qmr_supported_bf16_quantization", "qmr_set_gemv_plan", "qmr_gemv_plan",
+    "qmr_supported_bf16_quantization", "qmr_set_gemv_plan", "qmr_gemv_plan", "qmr_wide_address_extent",
     "qmr_last_kernel", "qmr_last_hip_kernel", "qmr_device_max_lds",
     # include/qmr_checkpoint.h
     "qmr_checkpoint_open", "qmr_checkpoint_close", "qmr_checkpoint_tensor_count",
@@ -136,6 +136,7 @@ def lib() -> C.CDLL:
         "qmr_buffer_release": (None, [vp]),
         "qmr_command_begin": (C.c_int, [vp, C.POINTER(vp)]),
         "qmr_encode": (C.c_int, [vp, C.c_char_p, C.POINTER(vp), szp, sz, u32p, sz, sz, sz]),
+        "qmr_wide_address_extent": (C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64)]),
         "qmr_encode_static": (C.c_int, [vp, C.c_char_p, C.POINTER(vp), szp, sz, u32p, sz, sz, sz]),
         "qmr_command_mark": (C.c_int, [vp, C.POINTER(C.c_int)]),
         "qmr_command_finish": (C.c_int, [vp, C.POINTER(_Timing)]),
@@ -189,6 +190,15 @@ def _s(v: Optional[str]) -> Optional[bytes]:
 
 
 # ---- host-only contract (no GPU needed) ----
+
+def wide_address_extent(rows: int, cols: int, batch: int, row_tiles: int) -> tuple[int, int, int, int]:
+    """qmr_wide_address_extent: (largest end of the wide kernel's in-range code
+    loads, code view bytes, largest end of its in-range image loads, image
+    workspace bytes), walked on the host."""
+    out = (C.c_uint64 * 4)()
+    _check(lib().qmr_wide_address_extent(rows, cols, batch, row_tiles, out))
+    return tuple(int(v) for v in out)
+
 
 def dispatch_layout(name: str, params: Sequence[int]) -> tuple[list[int], int]:
     """dispatch_layout (src/gpu.rs:1041-1294) for the matrix kernels."""

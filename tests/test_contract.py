@@ -244,3 +244,18 @@ def test_pack_bf16_exact_patterns_and_supported_formats():
             assert qmr.supported_bf16_quantization(bits, group)
     for bits, group in ((2, 64), (16, 64), (4, 8), (4, 256), (8, 0)):
         assert not qmr.supported_bf16_quantization(bits, group)
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(17408, 5120, 128), (17408, 5120, 256), (5120, 17408, 64),
+                                             (16 * 17 * 3 + 5, 512, 33), (9, 256, 1), (300, 1024, 200)])
+@pytest.mark.parametrize("row_tiles", [8, 17])
+def test_wide_kernel_loads_stay_inside_their_views(rows, cols, batch, row_tiles):
+    """Every code, x-fragment and group-sum load of the wide contraction
+    kernel (walked on the host through the kernel's own offset functions):
+    loads outside a view go through the vector offset past every view, and
+    the in-range ones end inside theirs. The last code byte and the last
+    image byte are reached, so the walk covers the views to their ends."""
+    code_end, code_extent, image_end, image_extent = qmr.wide_address_extent(rows, cols, batch, row_tiles)
+    assert code_end == code_extent == rows * cols // 2
+    assert image_extent == (cols // 64) * ((batch + 31) // 32) * 8448
+    assert image_end <= image_extent and image_end > image_extent - 8448
