@@ -88,16 +88,18 @@ uint32_t oracle_code(const uint32_t *w, size_t cols, uint32_t bits, size_t row, 
 }
 
 /* Row dequantisation (the embedding kernels, kernels/qwen.metal:73-77 and
- * kernels/affine_bf16.metal:162-174): y[c] = float(q)*s + b. q*s is exact in
- * FP32 for q < 2^8 and metadata with <= 24 significant bits, so the product
- * never rounds and the single correctly rounded result is RN32(q*s + b),
- * which fmaf computes exactly. */
+ * kernels/affine_bf16.metal:162-174): y[c] = float(q)*s + b, the product and
+ * the sum each rounded to FP32. (With BF16 or F16 metadata the product is
+ * exact, so this is also RN32(q*s + b).) */
 void oracle_dequant_row(const uint32_t *w, const void *s, const void *b, int kind,
                         size_t row, size_t cols, uint32_t bits, size_t group, float *out) {
     for (size_t c = 0; c < cols; ++c) {
         uint32_t q = oracle_code(w, cols, bits, row, c);
         size_t gi = row * (cols / group) + c / group;
-        out[c] = fmaf((float)q, oracle_meta(s, gi, kind), oracle_meta(b, gi, kind));
+        /* float(q) * s + b with each operation rounded (kernels/qwen.metal:40-47,
+         * 73-77); the Makefile builds with -ffp-contract=off. */
+        const float prod = (float)q * oracle_meta(s, gi, kind);
+        out[c] = prod + oracle_meta(b, gi, kind);
     }
 }
 

@@ -80,10 +80,8 @@ struct MfmaParams {
     float eps;
 };
 
-// Order this wave's earlier global writes before what follows, without the
-// device-scope fence (which writes back and invalidates the L2). Visibility
-// across XCDs comes from the agent-scope atomic stores and loads, which go
-// through the caches.
+// This wave's earlier global writes complete before what follows (ahead of
+// the workgroup barrier that precedes a split's arrival).
 __device__ __forceinline__ void vmem_order() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
@@ -337,16 +335,18 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         if (t0 + 1 < B)
             __hip_atomic_store(part + size_t(t0 + 1) * p.rows + row, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // The workgroup's partial stores happen before the barrier, which
+    // happens before thread 0's arrival; the arrival is an agent-scope
+    // acquire-release, so the band's last arriver (whose barrier follows its
+    // own acquire) reads every partial of the splits that arrived before it.
     vmem_order();
     __syncthreads();
     if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&p.counters[band], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t prev = __hip_atomic_fetch_add(&p.counters[band], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         *ldsLast = prev == nmat * p.ns - 1 ? 1 : 0;
     }
     __syncthreads();
     if (*ldsLast == 0) return;
-    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     const uint32_t band_rows = RT * 16;
     // MLP: 1/rms of each x[t] (the staged x carried the norm weights only),
     // from sum(x^2) over all columns, reduced through LDS (the operand area

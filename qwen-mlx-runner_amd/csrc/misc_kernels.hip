@@ -70,8 +70,11 @@ __global__ __launch_bounds__(256) void affine_generic_kernel(
     if (lane == 0) y[size_t(t) * rows + row] = v;
 }
 
-// y[c] = RN32(q*s + b). q*s is exact in FP32 (q < 2^8, s with <= 24
-// significant bits), so the fused form equals the reference's mul-then-add.
+// y[c] = RN32(RN32(q*s) + b), the reference's float(q) * s + b with each
+// operation rounded (kernels/qwen.metal:40-47,73-77). With BF16 or F16
+// metadata q*s is exact (at most 8 + 11 significant bits), so this equals
+// RN32(q*s + b); with FP32 metadata the product is rounded first, so no
+// fused multiply-add is used.
 __global__ __launch_bounds__(256) void embed_affine_kernel(
     const uint32_t *__restrict__ w, const void *__restrict__ s, const void *__restrict__ b,
     int meta, uint32_t row, uint32_t cols, uint32_t bits, uint32_t group, float *__restrict__ y) {
@@ -81,7 +84,11 @@ __global__ __launch_bounds__(256) void embed_affine_kernel(
     const uint32_t word = w[size_t(row) * (cols / pack) + c / pack];
     const uint32_t q = (word >> ((c % pack) * bits)) & ((1u << bits) - 1u);
     const size_t gi = size_t(row) * (cols / group) + c / group;
-    y[c] = __builtin_fmaf(float(q), meta_at(s, gi, meta), meta_at(b, gi, meta));
+    {
+#pragma clang fp contract(off)
+        const float prod = float(q) * meta_at(s, gi, meta);
+        y[c] = prod + meta_at(b, gi, meta);
+    }
 }
 
 // Dense F16 weights times token-major FP32 x; one wave per (row, rhs).

@@ -341,3 +341,29 @@ def test_mlp_oracle_matches_a_scalar_brute_force():
             g, u = product(mats[0], n, r), product(mats[1], n, r)
             want = g / (1.0 + math.exp(-g)) * u
             assert abs(got[t * rows + r] - want) <= 1e-12 * max(1.0, abs(want)), (t, r)
+
+
+def test_dequant_row_rounds_product_then_sum_for_fp32_metadata():
+    """kernels/qwen.metal:40-47 writes float(q) * s[gi] + b[gi]: with FP32
+    metadata the product (up to 8 + 24 significant bits) is rounded before the
+    sum. The oracle's row equals numpy's float32 multiply then add (each op
+    rounded) for every element, and differs from the single-rounding
+    RN32(q*s + b) on some, so the check tells the two apart."""
+    rng = np.random.default_rng(17)
+    rows, cols, bits, group = 3, 4096, 8, 32
+    w = rng.integers(0, 2**32, rows * cols * bits // 32, dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(0.001, 0.02, rows * cols // group).astype(np.float32)
+    b = rng.uniform(-1.0, 1.0, rows * cols // group).astype(np.float32)
+    shifts = (np.arange(cols) % (32 // bits)) * bits
+    fused_differs = 0
+    for r in range(rows):
+        words = w.reshape(rows, -1)[r][np.arange(cols) // (32 // bits)]
+        q = ((words >> shifts.astype(np.uint32)) & ((1 << bits) - 1)).astype(np.float32)
+        sg = s.reshape(rows, -1)[r][np.arange(cols) // group]
+        bg = b.reshape(rows, -1)[r][np.arange(cols) // group]
+        want = (q * sg) + bg  # float32 ops, each rounded
+        fused = (q.astype(np.float64) * sg.astype(np.float64) + bg.astype(np.float64)).astype(np.float32)
+        got = oracle.dequant_row(w, s, b, "f32", r, cols, bits, group)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), r
+        fused_differs += int(np.count_nonzero(fused != want))
+    assert fused_differs > 0
