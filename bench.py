@@ -527,6 +527,9 @@ def main() -> int:
     ap.add_argument("--no-loader", action="store_true", help="skip the checkpoint-loader timing")
     ap.add_argument("--no-config3", action="store_true",
                     help="skip the config-3 Q8 projection and vocabulary head")
+    ap.add_argument("--gemv-plan", default=None, metavar="RR,KS",
+                    help="force the GEMV kernel and tiling (qmr_set_gemv_plan) for the metric shapes, "
+                         "e.g. -1,0 for the vector-ALU kernel (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run plain copies of MIB MiB (counter calibration for profiling)")
     args = ap.parse_args()
@@ -540,6 +543,10 @@ def main() -> int:
 
     gpu = qmr.Gpu("aligned")
     log(f"bench: device {gpu.name()}, steps={args.steps} warmup={args.warmup} copies={args.copies}")
+    if args.gemv_plan:
+        rr, ks = (int(v) for v in args.gemv_plan.split(","))
+        gpu.set_gemv_plan(rr, ks)
+        log(f"bench: forced GEMV plan ({rr}, {ks})")
     if args.copy_calibration:
         copy_calibration(gpu, args.copy_calibration, 8)
     shapes = [] if args.only_wide else [("down", synth.MLP_SHAPES["down"])]
@@ -588,6 +595,8 @@ def main() -> int:
             log(f"bench:   read floor {floor['us_mean']} us ({floor['gbps']} GB/s)")
         del mats
 
+    if args.gemv_plan:
+        gpu.set_gemv_plan(0, 0)
     wide = [] if args.only_metric else bench_wide(gpu, args)
     if args.only_wide:
         print(json.dumps({"wide": wide}), flush=True)
@@ -644,6 +653,7 @@ def main() -> int:
         },
         "read_floor": floor,
         "cpu_baseline": cpu,
+        "gemv_plan_forced": args.gemv_plan,
         "results": results,
         "config3": config3,
         "mlp": mlp,

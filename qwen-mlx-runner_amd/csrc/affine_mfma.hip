@@ -335,18 +335,25 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         if (t0 + 1 < B)
             __hip_atomic_store(part + size_t(t0 + 1) * p.rows + row, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // The workgroup's partial stores happen before the barrier, which
-    // happens before thread 0's arrival; the arrival is an agent-scope
-    // acquire-release, so the band's last arriver (whose barrier follows its
-    // own acquire) reads every partial of the splits that arrived before it.
+    // Publication order without an agent-scope release or acquire (on gfx950
+    // these write back or invalidate the whole L2, which at the metric shape
+    // took the kernel from 15 to 37 us): the partials are agent-scope atomic
+    // stores, which the hardware writes through to the memory-side coherence
+    // point, and vmem_order waits until every one of them is acknowledged
+    // (vmcnt(0)) before the barrier; only then does thread 0 increment the
+    // band's counter. The last arriver reads the partials with agent-scope
+    // atomic loads, which bypass the non-coherent caches, after it has seen
+    // the final count, so each load returns the acknowledged value.
     vmem_order();
     __syncthreads();
     if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&p.counters[band], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t prev = __hip_atomic_fetch_add(&p.counters[band], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *ldsLast = prev == nmat * p.ns - 1 ? 1 : 0;
     }
     __syncthreads();
     if (*ldsLast == 0) return;
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     const uint32_t band_rows = RT * 16;
     // MLP: 1/rms of each x[t] (the staged x carried the norm weights only),
     // from sum(x^2) over all columns, reduced through LDS (the operand area
