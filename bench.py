@@ -271,6 +271,12 @@ def bench_config3(gpu: qmr.Gpu, args) -> list:
                 f"{100 * r['roofline']['frac']:.1f}% of peak ({r['kernel']})")
             out.append(r)
             del bufsets, ys, xb
+        floor = read_floor(gpu, m, mats, args, steps=args.config3_steps)
+        log(f"bench:   {tag} read floor {floor['us_mean']} us ({floor['gbps']} GB/s)")
+        for r in out:
+            if r["tag"] == tag:
+                r["read_floor_us"] = floor["us_mean"]
+                r["frac_of_floor"] = round(floor["us_mean"] / r["us_mean"], 4)
         del mats
     return out
 
@@ -464,7 +470,7 @@ def hip_kernel(plan) -> str:
             -3: "affine_rows_kernel"}.get(plan[0], "affine_gemv_kernel")
 
 
-def read_floor(gpu: qmr.Gpu, m: synth.PackedMatrix, mats, args) -> dict:
+def read_floor(gpu: qmr.Gpu, m: synth.PackedMatrix, mats, args, steps: int = 0) -> dict:
     """The streaming-read floor of the metric launch: read_checksum (16-byte
     non-temporal loads over contiguous per-workgroup slices, XOR-reduced into
     4096 slots) reads the same codes, scales and biases over the same
@@ -476,7 +482,7 @@ def read_floor(gpu: qmr.Gpu, m: synth.PackedMatrix, mats, args) -> dict:
     bufsets = [[w, s, b, o] for (w, s, b), o in zip(mats, outs)]
     params = [m.w.nbytes, m.s.nbytes, m.b.nbytes]
     log(f"bench: read floor, read_checksum of {m.nbytes} bytes ({len(mats)} rotating copies)")
-    mean_ms, _, durs = time_kernel(gpu, "read_checksum", bufsets, params, args.steps, args.warmup)
+    mean_ms, _, durs = time_kernel(gpu, "read_checksum", bufsets, params, steps or args.steps, args.warmup)
     want = np.uint32(0)
     for a in (m.w, m.s, m.b):
         want ^= np.bitwise_xor.reduce(np.ascontiguousarray(a).view(np.uint32))
