@@ -115,10 +115,17 @@ __device__ __forceinline__ float meta_hi(uint32_t v) {
     return float(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v >> 16)));
 }
 
-// DPP lane exchange inside 16-lane rows.
+// DPP lane exchange inside 16-lane rows. Every pattern used here reads a
+// lane of the reader's own row, so with full row and bank masks no lane reads
+// an invalid source and bound_ctrl changes nothing; it lets the compiler fold
+// the exchange into the add or max that consumes it (v_add_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xF, 0xF, true));
 }
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
@@ -127,22 +134,44 @@ constexpr int kDppMirror = 0x140;     // lane i <- 15 - i within 16 lanes
 
 // Sum and max over N (4, 8 or 16) consecutive, aligned lanes; every lane of
 // the run receives both. After the quad steps a quad holds one value, so the
-// mirrors pair each quad (then each half) with the other one.
+// mirrors pair each quad (then each half) with the other one. mx is a max of
+// magnitudes: a non-negative float, whose bits order as unsigned integers,
+// so its max runs on the bits (no NaN quieting between the steps).
 template <int N>
 __device__ __forceinline__ void group_reduce(float &sum, float &mx) {
     static_assert(N == 4 || N == 8 || N == 16, "runs of 4, 8 or 16 lanes");
+    uint32_t m = __float_as_uint(mx);
     sum += dpp_f32<kDppXor1>(sum);
-    mx = fmaxf(mx, dpp_f32<kDppXor1>(mx));
+    m = max(m, dpp_u32<kDppXor1>(m));
     sum += dpp_f32<kDppXor2>(sum);
-    mx = fmaxf(mx, dpp_f32<kDppXor2>(mx));
+    m = max(m, dpp_u32<kDppXor2>(m));
     if constexpr (N >= 8) {
         sum += dpp_f32<kDppHalfMirror>(sum);
-        mx = fmaxf(mx, dpp_f32<kDppHalfMirror>(mx));
+        m = max(m, dpp_u32<kDppHalfMirror>(m));
     }
     if constexpr (N >= 16) {
         sum += dpp_f32<kDppMirror>(sum);
-        mx = fmaxf(mx, dpp_f32<kDppMirror>(mx));
+        m = max(m, dpp_u32<kDppMirror>(m));
     }
+    mx = __uint_as_float(m);
+}
+
+// f16 conversions with one rounding (v_fma_mix*_f16: the FP32 fma a*b + c,
+// rounded to nearest even into one half of the result). The low-half forms
+// start a fresh word; the high-half forms keep the word's low half.
+//   hi_pair: (f16(a0*s), f16(a1*s))
+//   lo_pair: (f16(a0*s - h.lo), f16(a1*s - h.hi)) for the f16 pair h
+__device__ __forceinline__ uint32_t hi_pair(float a0, float a1, float s) {
+    uint32_t d;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a0), "v"(s));
+    asm("v_fma_mixhi_f16 %0, %1, %2, 0" : "+v"(d) : "v"(a1), "v"(s));
+    return d;
+}
+__device__ __forceinline__ uint32_t lo_pair(float a0, float a1, float s, uint32_t h) {
+    uint32_t d;
+    asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,0,1]" : "=v"(d) : "v"(a0), "v"(s), "v"(h));
+    asm("v_fma_mixhi_f16 %0, %1, %2, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "+v"(d) : "v"(a1), "v"(s), "v"(h));
+    return d;
 }
 
 // Staged activations of a run of K tiles, in LDS:
@@ -196,12 +225,11 @@ __device__ __forceinline__ void stage_x_item(const float (&xv)[8], uint32_t it, 
     constexpr int NGM = kTileK / GROUP;
     constexpr int HALF = 16 / NGM / 2;
     const ItemPos q = item_pos<B>(it);
-    float psum = 0.f, mx = 0.f;
+    // The item's sum (pairwise) and max |x|, then the group's.
+    float psum = ((xv[0] + xv[1]) + (xv[2] + xv[3])) + ((xv[4] + xv[5]) + (xv[6] + xv[7]));
+    float mx = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        psum += xv[j];
-        mx = fmaxf(mx, fabsf(xv[j]));
-    }
+    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(xv[j]));
     group_reduce<GROUP / 8>(psum, mx);
     const uint32_t mb = __float_as_uint(mx);
     int e = 0;
@@ -209,17 +237,16 @@ __device__ __forceinline__ void stage_x_item(const float (&xv)[8], uint32_t it, 
         e = int(mb >> 23) - 127 - 14;  // max * 2^-e in [2^14, 2^15) for normal max
         e = e < -100 ? -100 : (e > 100 ? 100 : e);
     }
+    // x * 2^-e is exact (a power of two, within FP32's normal range), so hi is
+    // its f16 rounding and lo the f16 rounding of the exact remainder.
     const float sc = __uint_as_float(uint32_t(127 - e) << 23);
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) {
-        // Packed round-to-nearest conversions (v_cvt_pk_f16_f32).
-        const float v0 = xv[k_of<BITS>(2 * e2)] * sc;
-        const float v1 = xv[k_of<BITS>(2 * e2 + 1)] * sc;
-        const h2 hh = __builtin_convertvector(f2{v0, v1}, h2);
-        const h2 ll = __builtin_convertvector(f2{v0 - static_cast<float>(hh.x), v1 - static_cast<float>(hh.y)}, h2);
-        hw[e2] = __builtin_bit_cast(uint32_t, hh);
-        lw[e2] = __builtin_bit_cast(uint32_t, ll);
+        const float v0 = xv[k_of<BITS>(2 * e2)];
+        const float v1 = xv[k_of<BITS>(2 * e2 + 1)];
+        hw[e2] = hi_pair(v0, v1, sc);
+        lw[e2] = lo_pair(v0, v1, sc, hw[e2]);
     }
     if (store) {
         u4 *dst = ldsA + ((q.Tl * 4 + q.m) * 4 + q.g) * (2 * B) + 2 * q.t;
