@@ -573,7 +573,12 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     //   0.5 |log2(waves / two per SIMD)|
     //   + log2(workgroups per CU rounded up / the even share)
     //   + x bytes read from L2 (once per band) / weight bytes
-    //   + 0.2 for a two-entry ring.
+    //   + 0.2 for a two-entry ring
+    //   + 1 when more than 64 KB of codes are in flight per CU (waves per
+    //     CU x ring x 2 KB entries): past that the stream slows, measured at
+    //     17408x5120 (B=1: 13.2 us with 34 KB against 13.9 with 68 KB; B=3:
+    //     15.3 us with 51 KB against 15.7 with 102 KB) and 12288x4096 (8.9
+    //     against 10.4 us at B=1, 48 KB against 96).
     double best = 1e30;
     for (uint32_t ring : {2u, 4u}) {
         if (force_ring && ring != force_ring) continue;
@@ -615,6 +620,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                     score += std::log2(per_cu);
                     score += double(nbands) * a.batch * a.cols * 4.0 / wbytes;
                     score += ring == 2 ? 0.2 : 0.0;
+                    if (waves / cus * ring * 2048.0 > 65536.0) score += 1.0;
                     if (score < best - 1e-9) {
                         best = score;
                         pl.kw = kw;
