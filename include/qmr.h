@@ -227,7 +227,7 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *            slot and a K-split of `ks`.
  *   rr = -4: row-band matrix-core kernel (the default where it has a plan
  *            whose workgroups are all resident at once); ks = ring*100000 +
- *            ns*10000 + tr*100 + kw pins its ring depth (2 or 4), K splits,
+ *            ns*10000 + tr*100 + kw pins its ring depth (2, 3 or 4), K splits,
  *            row tiles per band and waves per tile; zero fields and ks = 0
  *            leave them to its planner.
  * Shapes a forced kernel does not support fall back to the next one; pairs

@@ -420,6 +420,9 @@ hipError_t launch_xi(const BandParams &p, const TilePlan &pl, hipStream_t stream
     if (pl.ring >= 4)
         return resid ? launch_inst<BITS, META, GROUP, B, XI, 4, true>(p, pl, stream)
                      : launch_inst<BITS, META, GROUP, B, XI, 4, false>(p, pl, stream);
+    if (pl.ring == 3)
+        return resid ? launch_inst<BITS, META, GROUP, B, XI, 3, true>(p, pl, stream)
+                     : launch_inst<BITS, META, GROUP, B, XI, 3, false>(p, pl, stream);
     return resid ? launch_inst<BITS, META, GROUP, B, XI, 2, true>(p, pl, stream)
                  : launch_inst<BITS, META, GROUP, B, XI, 2, false>(p, pl, stream);
 }
@@ -473,10 +476,12 @@ const void *instance_group(uint32_t batch, uint32_t xi, uint32_t ring) {
     auto pick = [&](auto bconst) -> const void * {
         constexpr int B = decltype(bconst)::value;
         if (xi <= 4)
-            return ring >= 4 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 4, false>)
-                             : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 2, false>);
-        return ring >= 4 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 4, false>)
-                         : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 2, false>);
+            return ring >= 4   ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 4, false>)
+                   : ring == 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 3, false>)
+                               : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 2, false>);
+        return ring >= 4   ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 4, false>)
+               : ring == 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 3, false>)
+                           : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 2, false>);
     };
     switch (batch) {
         case 1: return pick(std::integral_constant<int, 1>{});
@@ -568,19 +573,19 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     const double wbytes = double(a.rows) * row_bytes + 2.0 * a.rows * (a.cols / a.group) * mb;
     // Candidates: ring depth, K splits, tiles per band, waves per tile. Every
     // workgroup must be resident in one round (a second round repeats the
-    // start-up latency). Score, fitted to timings of 160 shapes at
-    // 5120x17408 and 17408x5120 (B=1 and B=3) on MI355X:
+    // start-up latency). Score, fitted to timings on MI355X of every feasible
+    // plan of six shapes (5120x17408, 17408x5120 and 12288x4096 Q4,
+    // 17408x5120 Q8, 5120x5120 Q4 and Q8) at B=1 and B=3:
     //   0.5 |log2(waves / two per SIMD)|
     //   + log2(workgroups per CU rounded up / the even share)
     //   + x bytes read from L2 (once per band) / weight bytes
-    //   + 0.2 for a two-entry ring
-    //   + 1 when more than 64 KB of codes are in flight per CU (waves per
-    //     CU x ring x 2 KB entries): past that the stream slows, measured at
-    //     17408x5120 (B=1: 13.2 us with 34 KB against 13.9 with 68 KB; B=3:
-    //     15.3 us with 51 KB against 15.7 with 102 KB) and 12288x4096 (8.9
-    //     against 10.4 us at B=1, 48 KB against 96).
+    //   + |log2(codes in flight per CU / 36 KB)|, with waves per CU x ring
+    //     x 2 KB entries in flight: the stream is fastest near 36 KB and
+    //     slows with less (latency not covered) and with more (at 5120x17408
+    //     B=1: 12.2 us with 30 KB, 11.9 with 45, 12.3 with 60)
+    //   + 0.1 for a two-entry ring.
     double best = 1e30;
-    for (uint32_t ring : {2u, 4u}) {
+    for (uint32_t ring : {2u, 3u, 4u}) {
         if (force_ring && ring != force_ring) continue;
         for (uint32_t ns = 1; ns <= 4; ++ns) {
             if (force_ns && ns != force_ns) continue;
@@ -619,8 +624,8 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                     double score = 0.5 * std::fabs(std::log2(waves / (2.0 * 4 * cus)));
                     score += std::log2(per_cu);
                     score += double(nbands) * a.batch * a.cols * 4.0 / wbytes;
-                    score += ring == 2 ? 0.2 : 0.0;
-                    if (waves / cus * ring * 2048.0 > 65536.0) score += 1.0;
+                    score += std::fabs(std::log2(waves / cus * ring * 2048.0 / 36864.0));
+                    score += ring == 2 ? 0.1 : 0.0;
                     if (score < best - 1e-9) {
                         best = score;
                         pl.kw = kw;
