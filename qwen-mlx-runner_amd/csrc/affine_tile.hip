@@ -73,18 +73,16 @@ struct BandParams {
     uint32_t tr, kw, ns, nbands;
     uint32_t n_entries;   // 128-byte code entries per row (the last may be partial)
     uint32_t tiles;       // 128-column K tiles
-    uint32_t align_e;     // split boundaries are multiples of this many entries
     uint32_t gp;          // LDS pitch of a row's staged metadata (odd)
     uint32_t meta_bytes;  // LDS bytes of the staged metadata (16-byte multiple)
     uint32_t img_bytes;   // LDS bytes of the staged x images
 };
 
-// First entry of split s (aligned; the last split ends at n_entries).
-__device__ __forceinline__ uint32_t split_begin(uint32_t s, uint32_t ns, uint32_t n_entries, uint32_t align) {
+// First entry of split s (the last split ends at n_entries): splits differ
+// by at most one entry.
+__device__ __forceinline__ uint32_t split_begin(uint32_t s, uint32_t ns, uint32_t n_entries) {
     if (s >= ns) return n_entries;
-    const uint32_t raw = uint32_t((uint64_t(s) * n_entries) / ns);
-    const uint32_t a = (raw + align / 2) / align * align;
-    return a < n_entries ? a : n_entries;
+    return uint32_t((uint64_t(s) * n_entries) / ns);
 }
 
 template <int BITS, int GROUP, int B>
@@ -125,17 +123,21 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const uint32_t nG = p.cols / GROUP;
     const uint32_t Gp = p.gp;
     // The split's entries, tiles, groups and columns.
-    const uint32_t SE0 = split_begin(split, p.ns, p.n_entries, p.align_e);
-    const uint32_t SE1 = split_begin(split + 1, p.ns, p.n_entries, p.align_e);
+    const uint32_t SE0 = split_begin(split, p.ns, p.n_entries);
+    const uint32_t SE1 = split_begin(split + 1, p.ns, p.n_entries);
     const uint32_t ST0 = SE0 * TPE;
     const uint32_t ST1 = min(SE1 * TPE, p.tiles);
     const uint32_t nT = ST1 - ST0;
     const uint32_t G0 = ST0 * NGM;
     const uint32_t G1 = min(ST1 * NGM, nG);
-    // This wave's entries.
+    // This wave's entries. The bounds are wave-uniform, but the split
+    // arithmetic above divides in 64 bits, which the compiler lowers to
+    // vector instructions: readfirstlane keeps them in scalar registers, so
+    // the entry offset below is a scalar soffset and not a per-lane value
+    // that would put every code load in a readfirstlane loop.
     const uint32_t nSE = SE1 - SE0;
-    const uint32_t E0 = SE0 + kw * nSE / KW;
-    const uint32_t E1 = SE0 + (kw + 1) * nSE / KW;
+    const uint32_t E0 = __builtin_amdgcn_readfirstlane(SE0 + kw * nSE / KW);
+    const uint32_t E1 = __builtin_amdgcn_readfirstlane(SE0 + (kw + 1) * nSE / KW);
 
     uint32_t *ldsM = reinterpret_cast<uint32_t *>(lds);  // [tr*16][Gp] s|b<<16, or [tr*16][Gp][2] f32
     unsigned char *img = lds + p.meta_bytes;              // [nT] tile images
@@ -163,16 +165,21 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     }
 
     // ---- 2. Metadata of the band's rows over the split's groups: one run
-    // per row and plane, as 16-byte loads when the runs are 16-byte aligned
-    // (every checkpoint shape with aligned splits). Rows past the matrix read
-    // zeros through the buffer range check. ----
-    const uint32_t run_bytes = (G1 - G0) * MB;
-    const bool vec_meta = (nG * MB) % 16 == 0 && (G0 * MB) % 16 == 0 && run_bytes % 16 == 0;
-    const uint32_t upr = vec_meta ? run_bytes / 16 : 0u;  // units per row
+    // per row and plane, as 16-byte loads when the rows are 16-byte aligned
+    // (every checkpoint shape). A run covers groups [Ga, Gb): G0 rounded down
+    // and G1 rounded up to whole 16-byte units, both inside the row (nG is a
+    // multiple of VEC); the `lead` groups before G0 and those past G1 are
+    // read and dropped, so splits may start at any entry. Rows past the
+    // matrix read zeros through the buffer range check. ----
+    const bool vec_meta = (nG * MB) % 16 == 0;
+    const uint32_t lead = G0 % uint32_t(VEC);
+    const uint32_t Ga = G0 - lead;
+    const uint32_t Gb = (G1 + uint32_t(VEC) - 1) / uint32_t(VEC) * uint32_t(VEC);
+    const uint32_t upr = vec_meta ? (Gb - Ga) / uint32_t(VEC) : 0u;  // units per row
     const uint32_t units = p.tr * 16u * upr;
     auto unit_off = [&](uint32_t f) -> uint32_t {
         const uint32_t rl = f / upr;
-        return ((band_row0 + rl) * nG + G0) * MB + (f - rl * upr) * 16u;
+        return ((band_row0 + rl) * nG + Ga) * MB + (f - rl * upr) * 16u;
     };
     u4 ms[kMetaUnits], mbv[kMetaUnits];
 #pragma unroll
@@ -220,24 +227,42 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- 4. Metadata to LDS. ----
+    // ---- 4. x as MFMA operand images (hi/lo f16, group sums, epilogue
+    // factors), tile by tile, as soon as x has landed: x was requested
+    // first and comes from L2, while the metadata behind it comes from HBM.
+    // ----
+    u4 *imgA = reinterpret_cast<u4 *>(img);
+    float4 *imgS = reinterpret_cast<float4 *>(img + nT * TIMG_A);
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
+        if (i > 0 && uint32_t(tid) - uint32_t(lane) + uint32_t(i * nthr) >= items) break;  // whole waves in or out
+        stage_x_item<BITS, GROUP, B>(xv[i], it, it < items, lane, imgA, imgS);
+    }
+    // ---- 5. Metadata to LDS. ----
     if (vec_meta) {
+        // Unit f holds groups g .. g+VEC-1 of its row (g relative to G0, so
+        // negative in the lead); only groups in [0, G1 - G0) are kept.
+        const uint32_t ng = G1 - G0;
         auto put = [&](uint32_t f, const u4 &sv, const u4 &bv) {
             const uint32_t rl = f / upr;
-            const uint32_t g = (f - rl * upr) * VEC;
+            const int g = int((f - rl * upr) * uint32_t(VEC)) - int(lead);
+            auto keep = [&](int gg) { return gg >= 0 && uint32_t(gg) < ng; };
             if constexpr (META == 0) {
-                uint32_t *dst = ldsM + (rl * Gp + g) * 2;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    dst[2 * e] = sv[e];
-                    dst[2 * e + 1] = bv[e];
+                    if (keep(g + e)) {
+                        uint32_t *dst = ldsM + (rl * Gp + uint32_t(g + e)) * 2;
+                        dst[0] = sv[e];
+                        dst[1] = bv[e];
+                    }
                 }
             } else {
-                uint32_t *dst = ldsM + rl * Gp + g;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    dst[2 * e] = __builtin_amdgcn_perm(bv[e], sv[e], 0x05040100u);
-                    dst[2 * e + 1] = __builtin_amdgcn_perm(bv[e], sv[e], 0x07060302u);
+                    if (keep(g + 2 * e)) ldsM[rl * Gp + uint32_t(g + 2 * e)] = __builtin_amdgcn_perm(bv[e], sv[e], 0x05040100u);
+                    if (keep(g + 2 * e + 1))
+                        ldsM[rl * Gp + uint32_t(g + 2 * e + 1)] = __builtin_amdgcn_perm(bv[e], sv[e], 0x07060302u);
                 }
             }
         };
@@ -284,16 +309,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         }
     }
 
-    // ---- 5. x as MFMA operand images (hi/lo f16, group sums, epilogue
-    // factors), tile by tile; zero sums and factors of absent RHS. ----
-    u4 *imgA = reinterpret_cast<u4 *>(img);
-    float4 *imgS = reinterpret_cast<float4 *>(img + nT * TIMG_A);
-#pragma unroll
-    for (int i = 0; i < XI; ++i) {
-        const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
-        if (i > 0 && uint32_t(tid) - uint32_t(lane) + uint32_t(i * nthr) >= items) break;  // whole waves in or out
-        stage_x_item<BITS, GROUP, B>(xv[i], it, it < items, lane, imgA, imgS);
-    }
+    // Zero sums and factors of absent RHS.
     stage_x_pads<GROUP, B>(nT, tid, nthr, imgS);
     lds_barrier();
 
@@ -461,11 +477,9 @@ hipError_t launch_meta(const BandParams &p, const TilePlan &pl, uint32_t group, 
     }
 }
 
-uint32_t host_split_begin(uint32_t s, uint32_t ns, uint32_t n_entries, uint32_t align) {
+uint32_t host_split_begin(uint32_t s, uint32_t ns, uint32_t n_entries) {
     if (s >= ns) return n_entries;
-    const uint32_t raw = uint32_t((uint64_t(s) * n_entries) / ns);
-    const uint32_t a = (raw + align / 2) / align * align;
-    return a < n_entries ? a : n_entries;
+    return uint32_t((uint64_t(s) * n_entries) / ns);
 }
 
 // The plain form's kernel instance for a format, x-item count and ring
@@ -567,7 +581,6 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     const uint32_t tpe = 8 / a.bits;
     const uint32_t tiles = (a.cols + kTileK - 1) / kTileK;
     const uint32_t mb = a.meta == Meta::F32 ? 4 : 2;
-    const uint32_t align_e = std::max(1u, 16u / (mb * tpe * ngm));
     const uint32_t cus = lim.num_cus > 0 ? uint32_t(lim.num_cus) : 256u;
     const size_t timg = size_t(4) * 4 * 2 * a.batch * 16 + size_t(ngm) * ((16 / ngm / 2) / 2) * 16;
     const double wbytes = double(a.rows) * row_bytes + 2.0 * a.rows * (a.cols / a.group) * mb;
@@ -589,12 +602,12 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
         if (force_ring && ring != force_ring) continue;
         for (uint32_t ns = 1; ns <= 4; ++ns) {
             if (force_ns && ns != force_ns) continue;
-            if (ns * align_e > n_entries) continue;
+            if (ns > n_entries) continue;
             uint32_t max_se = 0;
             bool empty = false;
             for (uint32_t sp = 0; sp < ns; ++sp) {
-                const uint32_t e0 = host_split_begin(sp, ns, n_entries, align_e);
-                const uint32_t e1 = host_split_begin(sp + 1, ns, n_entries, align_e);
+                const uint32_t e0 = host_split_begin(sp, ns, n_entries);
+                const uint32_t e1 = host_split_begin(sp + 1, ns, n_entries);
                 if (e1 <= e0) empty = true;
                 else max_se = std::max(max_se, e1 - e0);
             }
@@ -634,7 +647,6 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                         pl.nbands = nbands;
                         pl.n_entries = n_entries;
                         pl.tiles = tiles;
-                        pl.align_e = align_e;
                         pl.gp = gp;
                         pl.meta_bytes = uint32_t(meta);
                         pl.img_bytes = uint32_t(img);
@@ -678,7 +690,6 @@ hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned 
     p.nbands = pl.nbands;
     p.n_entries = pl.n_entries;
     p.tiles = pl.tiles;
-    p.align_e = pl.align_e;
     p.gp = pl.gp;
     p.meta_bytes = pl.meta_bytes;
     p.img_bytes = pl.img_bytes;

@@ -127,7 +127,6 @@ struct TilePlan {
     uint32_t nbands = 0;      // row bands
     uint32_t n_entries = 0;   // 128-byte entries per row
     uint32_t tiles = 0;       // 128-column K tiles
-    uint32_t align_e = 0;     // split boundaries are multiples of this many entries
     uint32_t gp = 0;          // LDS pitch of a row's metadata
     uint32_t meta_bytes = 0;  // LDS bytes of the staged metadata
     uint32_t img_bytes = 0;   // LDS bytes of the staged x images
