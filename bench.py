@@ -13,8 +13,11 @@ timed region starts. Weights rotate over --copies distinct copies so that the
 Timing: K launches run back to back between two HIP events recorded on the
 library's stream; their difference over K is the mean launch duration, and
 `value` is the algorithmic bytes of one launch (codes + scales + biases + x +
-y) divided by it. The wall time of that timed region (synchronised on both
-sides) gives ms_per_step. A second pass brackets each launch with its own
+y) divided by it. Ahead of the start event a one-wave kernel holds the stream
+for 40 us per launch (qmr_command_delay), so that all K launches are queued
+before the GPU reaches them and the events time the GPU, not the host's
+enqueue rate. The wall time of the timed region (synchronised on both sides)
+less that hold gives ms_per_step. A second pass brackets each launch with its own
 events to report the spread. Before the W warmup launches of each case, about
 1 s of untimed launches lets the GPU clocks settle after the host-side idle
 of building that case's matrix.
@@ -74,6 +77,7 @@ def log(msg: str) -> None:
 
 
 SETTLE_MS = 1000.0
+HOLD_US = 40  # GPU-side hold per timed launch, ahead of the start mark
 
 
 def settle(gpu: qmr.Gpu, name: str, bufsets, params, threads: int, ms: float) -> None:
@@ -110,22 +114,37 @@ def time_kernel(gpu: qmr.Gpu, name: str, bufsets, params, steps: int, warmup: in
         cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
     cmd.finish()
     cmd.release()
-    # Timed region: synchronised on both sides, K launches back to back.
+    # Timed region: synchronised on both sides, K launches back to back. A
+    # GPU-side hold ahead of the start mark (HOLD_US per launch) keeps the
+    # GPU from reaching the launches before the host has queued them all, so
+    # the marks time the GPU and not the host's enqueue rate (7-14 us per
+    # launch through this Python binding, which is slower than a 12 us GEMV
+    # on some hosts).
     cmd = gpu.begin()
+    hold_us = min(HOLD_US * steps, 1_000_000)
+    cmd.delay(hold_us)
     t0 = time.perf_counter()
     a = cmd.mark()
     for k in range(steps):
         cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
     b = cmd.mark()
+    enqueue_us = (time.perf_counter() - t0) * 1e6
     cmd.finish()
-    wall = time.perf_counter() - t0
+    # Wall time of the region less the hold, which the GPU starts as the host
+    # starts enqueueing: the K launches plus the synchronisation.
+    wall = time.perf_counter() - t0 - hold_us * 1e-6
     mean_ms = cmd.elapsed_ms(a, b) / steps
     cmd.release()
+    if enqueue_us > hold_us:
+        log(f"bench:   warning: enqueueing {steps} launches took {enqueue_us:.0f} us, longer than the "
+            f"{hold_us} us hold; the timing may include host gaps")
     # Spread: each launch bracketed by its own pair of events (adds the
     # event overhead to every sample, so these read a little high).
     cmd = gpu.begin()
     marks = []
-    for k in range(min(steps, 100)):
+    n = min(steps, 100)
+    cmd.delay(min(HOLD_US * 3 * n, 1_000_000))
+    for k in range(n):
         a = cmd.mark()
         cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
         marks.append((a, cmd.mark()))
@@ -318,6 +337,7 @@ def bench_mlp(gpu: qmr.Gpu, args) -> list:
         cmd.finish()
         cmd.release()
         cmd = gpu.begin()
+        cmd.delay(min(2 * HOLD_US * args.mlp_steps, 1_000_000))
         a = cmd.mark()
         for k in range(args.mlp_steps):
             cmd.encode("mlp_gate_up_swiglu_bf16", up_sets[k % copies], up_params, up_threads, 128)
@@ -338,6 +358,7 @@ def bench_mlp(gpu: qmr.Gpu, args) -> list:
             seq.append((name, [*mats["down"][k], xi, yd], [hidden, inter, 4, 64] + extra))
         thr = [qmr.dispatch_layout(n, p_)[1] for n, _, p_ in seq]
         cmd = gpu.begin()
+        cmd.delay(min(3 * HOLD_US * args.mlp_steps, 1_000_000))
         a = cmd.mark()
         for k in range(args.mlp_steps):
             for j in range(3):

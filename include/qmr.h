@@ -148,6 +148,13 @@ int qmr_encode_static(qmr_command *command, const char *name, qmr_buffer *const 
  * qmr_command_elapsed after the command finishes. (The Metal backend's
  * counterpart is the GPU start/end timestamp pair of FrameTiming.) */
 int qmr_command_mark(qmr_command *command, int *index);
+/* No counterpart in the reference (a measurement aid): enqueues one wave
+ * that holds the device stream for `microseconds` (at most 1,000,000) of
+ * the GPU's real-time clock. A benchmark calls it before its start mark so
+ * that the launches it enqueues next are all queued when the GPU reaches
+ * them, and the marks time them back to back whatever the host's enqueue
+ * rate. */
+int qmr_command_delay(qmr_command *command, uint32_t microseconds);
 /* Gpu::finish: synchronise, check status, fill timing (may be NULL). */
 int qmr_command_finish(qmr_command *command, qmr_frame_timing *timing);
 /* Milliseconds between two marks of a finished command. */
@@ -227,7 +234,7 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *            slot and a K-split of `ks`.
  *   rr = -4: row-band matrix-core kernel (the default where it has a plan
  *            whose workgroups are all resident at once); ks = ring*100000 +
- *            ns*10000 + tr*100 + kw pins its ring depth (2, 3 or 4), K splits,
+ *            ns*10000 + tr*100 + kw pins its ring depth (2 or 3), K splits,
  *            row tiles per band and waves per tile; zero fields and ks = 0
  *            leave them to its planner.
  * Shapes a forced kernel does not support fall back to the next one; pairs

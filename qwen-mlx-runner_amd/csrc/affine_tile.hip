@@ -433,20 +433,27 @@ hipError_t launch_inst(const BandParams &p, const TilePlan &pl, hipStream_t stre
 template <int BITS, int META, int GROUP, int B, int XI>
 hipError_t launch_xi(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
     const bool resid = p.r != nullptr;
-    if (pl.ring >= 4)
-        return resid ? launch_inst<BITS, META, GROUP, B, XI, 4, true>(p, pl, stream)
-                     : launch_inst<BITS, META, GROUP, B, XI, 4, false>(p, pl, stream);
-    if (pl.ring == 3)
+    if (pl.ring >= 3)
         return resid ? launch_inst<BITS, META, GROUP, B, XI, 3, true>(p, pl, stream)
                      : launch_inst<BITS, META, GROUP, B, XI, 3, false>(p, pl, stream);
     return resid ? launch_inst<BITS, META, GROUP, B, XI, 2, true>(p, pl, stream)
                  : launch_inst<BITS, META, GROUP, B, XI, 2, false>(p, pl, stream);
 }
 
+// x items per thread: the smallest compiled count that covers the plan's.
+// Every unrolled item issues its loads (dead ones read zeros), so the
+// metric shapes get exact counts: 2 at B=1 and 5 at B=3 (5120x17408, three
+// splits), each 0.15-0.2 us faster than rounding up to 4 and 8.
+constexpr uint32_t xi_instance(uint32_t xi) { return xi <= 2 ? 2 : xi <= 4 ? 4 : xi <= 5 ? 5 : 8; }
+
 template <int BITS, int META, int GROUP, int B>
 hipError_t launch_b(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
-    if (pl.xi <= 4) return launch_xi<BITS, META, GROUP, B, 4>(p, pl, stream);
-    return launch_xi<BITS, META, GROUP, B, 8>(p, pl, stream);
+    switch (xi_instance(pl.xi)) {
+        case 2: return launch_xi<BITS, META, GROUP, B, 2>(p, pl, stream);
+        case 4: return launch_xi<BITS, META, GROUP, B, 4>(p, pl, stream);
+        case 5: return launch_xi<BITS, META, GROUP, B, 5>(p, pl, stream);
+        default: return launch_xi<BITS, META, GROUP, B, 8>(p, pl, stream);
+    }
 }
 
 template <int BITS, int META, int GROUP>
@@ -489,13 +496,17 @@ const void *instance_group(uint32_t batch, uint32_t xi, uint32_t ring) {
     constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
     auto pick = [&](auto bconst) -> const void * {
         constexpr int B = decltype(bconst)::value;
-        if (xi <= 4)
-            return ring >= 4   ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 4, false>)
-                   : ring == 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 3, false>)
-                               : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 4, 2, false>);
-        return ring >= 4   ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 4, false>)
-               : ring == 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 3, false>)
-                           : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, 8, 2, false>);
+        auto by_ring = [&](auto xconst) -> const void * {
+            constexpr int XI = decltype(xconst)::value;
+            return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, false>)
+                             : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, false>);
+        };
+        switch (xi_instance(xi)) {
+            case 2: return by_ring(std::integral_constant<int, 2>{});
+            case 4: return by_ring(std::integral_constant<int, 4>{});
+            case 5: return by_ring(std::integral_constant<int, 5>{});
+            default: return by_ring(std::integral_constant<int, 8>{});
+        }
     };
     switch (batch) {
         case 1: return pick(std::integral_constant<int, 1>{});
@@ -598,7 +609,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     //     B=1: 12.2 us with 30 KB, 11.9 with 45, 12.3 with 60)
     //   + 0.1 for a two-entry ring.
     double best = 1e30;
-    for (uint32_t ring : {2u, 3u, 4u}) {
+    for (uint32_t ring : {2u, 3u}) {
         if (force_ring && ring != force_ring) continue;
         for (uint32_t ns = 1; ns <= 4; ++ns) {
             if (force_ns && ns != force_ns) continue;

@@ -66,6 +66,8 @@ hipError_t launch_embed_f16(const uint16_t *w, uint32_t row, uint32_t cols, floa
 hipError_t launch_copy_f32(const float *x, float *y, uint32_t n, int num_cus, hipStream_t stream);
 // p[i] = 0 for i < n (a fill kernel: safe to capture into a graph).
 hipError_t launch_zero_u32(uint32_t *p, uint32_t n, hipStream_t stream);
+// One wave that returns after `ticks` of the device's real-time counter.
+hipError_t launch_delay(unsigned long long ticks, hipStream_t stream);
 // One streaming read of three views (byte sizes, multiples of 4); out holds
 // kChecksumSlots u32 whose XOR is the XOR of every word read.
 hipError_t launch_read_checksum(const void *a, uint32_t na, const void *b, uint32_t nb, const void *c, uint32_t nc,

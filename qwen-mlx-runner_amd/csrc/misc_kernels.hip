@@ -325,6 +325,20 @@ hipError_t launch_read_checksum(const void *a, uint32_t na, const void *b, uint3
     return hipGetLastError();
 }
 
+// Holds the stream for `ticks` of the constant-rate real-time counter: one
+// wave polls the counter with long sleeps in between and always ends when
+// the interval has passed. A benchmark enqueues it before its start mark so
+// that every launch behind it is already queued when the GPU reaches them.
+__global__ __launch_bounds__(64) void delay_kernel(unsigned long long ticks) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(127);
+}
+
+hipError_t launch_delay(unsigned long long ticks, hipStream_t stream) {
+    hipLaunchKernelGGL(delay_kernel, dim3(1), dim3(64), 0, stream, ticks);
+    return hipGetLastError();
+}
+
 // Zero fill with vector stores (a kernel rather than hipMemsetAsync, so that
 // a command captured into a graph clears the memory on every replay).
 __global__ __launch_bounds__(256) void zero_u32_kernel(uint32_t *__restrict__ p, uint32_t n) {

@@ -344,7 +344,7 @@ qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a,
                                                         uint32_t(ks / 10000 % 10), uint32_t(ks / 100000))
                                 : qmr::plan_affine_tile(a, dev->limits);
     if (pl.kw > 0 && sched == BandSchedule::Shared) {
-        const qmr::TilePlan alt = qmr::plan_affine_tile(a, dev->limits, pl.kw, pl.tr, pl.ns, pl.ring == 4 ? 2 : 4);
+        const qmr::TilePlan alt = qmr::plan_affine_tile(a, dev->limits, pl.kw, pl.tr, pl.ns, pl.ring == 3 ? 2 : 3);
         if (alt.kw > 0) pl = alt;
     } else if (pl.kw > 0 && sched == BandSchedule::R2) {
         qmr::TilePlan alt;
@@ -732,6 +732,22 @@ int qmr_command_mark(qmr_command *command, int *index) {
         }
         command->marks.push_back(ev);
         if (index) *index = int(command->marks.size()) - 1;
+        return QMR_OK;
+    });
+}
+
+int qmr_command_delay(qmr_command *command, uint32_t microseconds) {
+    return guarded([&]() -> int {
+        ensure(command && !command->finished, "qmr_command_delay: command not open");
+        ensure(microseconds <= 1000000u, "qmr_command_delay: at most 1000000 microseconds");
+        check_hip(hipSetDevice(command->device->ordinal), "hipSetDevice");
+        int khz = 0;
+        check_hip(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, command->device->ordinal),
+                  "hipDeviceGetAttribute");
+        ensure(khz > 0, "qmr_command_delay: the device reports no real-time clock rate", QMR_ERR_DEVICE);
+        start_gpu(command->device);
+        check_hip(qmr::launch_delay(uint64_t(microseconds) * uint64_t(khz) / 1000u, command->device->stream),
+                  "delay launch");
         return QMR_OK;
     });
 }

@@ -42,7 +42,8 @@ EXPORTED_SYMBOLS = (
     "qmr_set_block_kernel_mode", "qmr_compact_metadata", "qmr_record_compacted_metadata",
     "qmr_metadata_stats", "qmr_buffer_alloc", "qmr_buffer_upload", "qmr_buffer_read",
     "qmr_buffer_write", "qmr_buffer_length", "qmr_buffer_retain", "qmr_buffer_release",
-    "qmr_command_begin", "qmr_encode", "qmr_encode_static", "qmr_command_mark", "qmr_command_finish",
+    "qmr_command_begin", "qmr_encode", "qmr_encode_static", "qmr_command_mark", "qmr_command_delay",
+    "qmr_command_finish",
     "qmr_command_elapsed", "qmr_command_release", "qmr_dispatch_layout",
     "qmr_checked_buffer_range", "qmr_ranges_overlap", "qmr_specialized_matvec",
     "qmr_specialized_matmul", "qmr_parse_block_kernel_mode", "qmr_pack_bf16_exact",
@@ -139,6 +140,7 @@ def lib() -> C.CDLL:
         "qmr_wide_address_extent": (C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64)]),
         "qmr_encode_static": (C.c_int, [vp, C.c_char_p, C.POINTER(vp), szp, sz, u32p, sz, sz, sz]),
         "qmr_command_mark": (C.c_int, [vp, C.POINTER(C.c_int)]),
+        "qmr_command_delay": (C.c_int, [vp, C.c_uint32]),
         "qmr_command_finish": (C.c_int, [vp, C.POINTER(_Timing)]),
         "qmr_command_elapsed": (C.c_int, [vp, C.c_int, C.c_int, C.POINTER(C.c_double)]),
         "qmr_command_release": (None, [vp]),
@@ -320,6 +322,12 @@ class Command:
         idx = C.c_int()
         _check(lib().qmr_command_mark(self._h, C.byref(idx)))
         return idx.value
+
+    def delay(self, microseconds: int) -> None:
+        """Hold the device stream for `microseconds` of GPU time (at most
+        1,000,000), so that launches encoded next are queued before the GPU
+        reaches them (a measurement aid; no reference counterpart)."""
+        _check(lib().qmr_command_delay(self._h, int(microseconds)))
 
     def finish(self) -> FrameTiming:
         t = _Timing()

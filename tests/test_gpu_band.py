@@ -7,7 +7,7 @@ Every shape is run under plans forced through the tuning hook (rr = -4,
 ks = ring*100000 + ns*10000 + tr*100 + kw) so that each code path is taken:
 one to four K splits (the last split adds the others' epoch-tagged sums),
 one to eight row tiles per band, one to eight waves per tile, two- and
-four-entry rings; row tails, K tails that end inside a tile or inside a
+three-entry rings; row tails, K tails that end inside a tile or inside a
 128-byte entry, Q8, groups 32/64/128, F32/BF16/F16 metadata, and metadata
 runs that are not 16-byte multiples (per-value staging path).
 """
@@ -69,8 +69,10 @@ CASES = [
     (24, 4096, 8, 32, 2, "bf16"),      # group 32, fewer rows than two tiles
     (260, 576, 4, 64, 1, "bf16"),      # 9 groups per row: per-value metadata staging
     (129, 1152, 8, 128, 3, "f32"),     # Q8/g128 FP32 metadata, one row past a tile
+    (96, 5120, 8, 128, 2, "bf16"),     # Q8/g128: three splits start at entries 13 and 26, so the
+                                       # 16-bit metadata runs start 5 and 2 groups past a 16-byte unit
 ]
-PLANS = [(2, 1, 1, 1), (4, 1, 2, 2), (2, 2, 4, 2), (4, 3, 4, 2), (4, 4, 2, 4), (2, 3, 8, 1), (2, 2, 1, 8)]
+PLANS = [(2, 1, 1, 1), (3, 1, 2, 2), (2, 2, 4, 2), (3, 3, 4, 2), (3, 4, 2, 4), (2, 3, 8, 1), (2, 2, 1, 8)]
 
 
 @pytest.mark.parametrize("rows,cols,bits,group,batch,kind", CASES)
@@ -96,7 +98,7 @@ def test_band_plans_match_fp64_oracle(gpu, rows, cols, bits, group, batch, kind)
 def test_forced_band_plans_are_taken(gpu):
     """The tuning hook reports the band kernel with the forced shape for the
     metric matrix (the report covers group 64 with BF16 metadata)."""
-    for ring, ns, tr, kw in [(4, 3, 4, 2), (2, 3, 4, 2), (4, 3, 2, 2), (2, 4, 2, 2)]:
+    for ring, ns, tr, kw in [(3, 3, 4, 2), (2, 3, 4, 2), (3, 3, 2, 2), (2, 4, 2, 2)]:
         gpu.set_gemv_plan(-4, _ks(ring, ns, tr, kw))
         try:
             rr, ks = gpu.gemv_plan(5120, 17408, 4, 1)
@@ -117,7 +119,7 @@ def test_split_sums_stay_correct_across_back_to_back_launches_of_different_shape
     workspace; each launch's last split must take only its own launch's sums
     (the epoch tag). Results are bit-identical to isolated launches."""
     rng = np.random.default_rng(7)
-    shapes = [(5120, 17408, 3, (4, 3, 4, 2)), (2048, 8192, 1, (2, 4, 2, 2)), (5120, 17408, 3, (4, 2, 4, 2)),
+    shapes = [(5120, 17408, 3, (3, 3, 4, 2)), (2048, 8192, 1, (2, 4, 2, 2)), (5120, 17408, 3, (3, 2, 4, 2)),
               (777, 4096, 2, (2, 3, 1, 4))]
     mats, xs, isolated = [], [], []
     for rows, cols, batch, (ring, ns, tr, kw) in shapes:
@@ -160,7 +162,7 @@ def test_band_kernel_is_deterministic_across_launches(gpu):
 
 
 @pytest.mark.parametrize("in_place", [False, True])
-@pytest.mark.parametrize("ring,ns,tr,kw", [(4, 3, 4, 2), (2, 2, 4, 2)])
+@pytest.mark.parametrize("ring,ns,tr,kw", [(3, 3, 4, 2), (2, 2, 4, 2)])
 def test_band_residual_form(gpu, in_place, ring, ns, tr, kw):
     """matmul_affine_add on the band kernel: y = r + W x, with y == r in place."""
     rng = np.random.default_rng([ring, ns, tr, kw, int(in_place)])

@@ -433,3 +433,33 @@ def test_embed_offset_writes_only_its_slot_bit_exact(gpu, name, bits, group):
     assert np.array_equal(got[slot], want.view(np.uint32)), name
     others = np.delete(got, slot, axis=0)
     assert np.all(others == guard), name
+
+
+def test_command_delay_holds_the_stream(gpu):
+    """qmr_command_delay (a measurement aid with no reference counterpart)
+    holds the device stream for the requested GPU time: marks around a
+    300 us hold read at least that, and launches queued behind it run after
+    it and stay correct. Requests above one second are rejected."""
+    m = synth.q4_bf16_matrix(1024, 1024, 5, tag="config0")
+    x = synth.activations(1024, 1, 5, tag="config0")
+    bufs = [gpu.upload_bytes(m.w), gpu.upload_bytes(m.s), gpu.upload_bytes(m.b), gpu.upload_f32(x.ravel()),
+            gpu.alloc_f32(1024)]
+    _, threads = qmr.dispatch_layout("matvec_affine_bf16", [1024, 1024, 4, 64])
+    cmd = gpu.begin()
+    a = cmd.mark()
+    cmd.delay(300)
+    b = cmd.mark()
+    cmd.encode("matvec_affine_bf16", bufs, [1024, 1024, 4, 64], threads, 128)
+    cmd.finish()
+    held = cmd.elapsed_ms(a, b)
+    cmd.release()
+    assert 0.29 <= held <= 50.0, held
+    want = oracle.matmul_f64(m.w, m.s, m.b, "bf16", x, 1024, 1024, 4, 64)
+    assert_gate(gpu.read_f32(bufs[4], 1024), want)
+    cmd = gpu.begin()
+    try:
+        with pytest.raises(qmr.QmrError, match="at most 1000000"):
+            cmd.delay(1_000_001)
+    finally:
+        cmd.finish()
+        cmd.release()
