@@ -76,14 +76,10 @@ struct BandParams {
     uint32_t gp;          // LDS pitch of a row's staged metadata (odd)
     uint32_t meta_bytes;  // LDS bytes of the staged metadata (16-byte multiple)
     uint32_t img_bytes;   // LDS bytes of the staged x images
+    uint32_t split_e[5];  // first entry of each split, then n_entries (host_split_begin)
+    uint32_t kw_shift;    // log2(kw)
+    uint32_t unit_shift;  // log2 of the threads per row in the metadata loads (>= units per row)
 };
-
-// First entry of split s (the last split ends at n_entries): splits differ
-// by at most one entry.
-__device__ __forceinline__ uint32_t split_begin(uint32_t s, uint32_t ns, uint32_t n_entries) {
-    if (s >= ns) return n_entries;
-    return uint32_t((uint64_t(s) * n_entries) / ns);
-}
 
 template <int BITS, int GROUP, int B>
 constexpr uint32_t tile_img_bytes() {
@@ -114,30 +110,33 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const int r = lane & 15;
     const int lg = lane >> 4;
     const uint32_t KW = p.kw;
-    const uint32_t ti = uint32_t(wave) / KW;
-    const uint32_t kw = uint32_t(wave) - ti * KW;
+    const uint32_t ti = uint32_t(wave) >> p.kw_shift;
+    const uint32_t kw = uint32_t(wave) & (KW - 1u);
     const uint32_t band = blockIdx.x % p.nbands;
     const uint32_t split = blockIdx.x / p.nbands;
     const uint32_t band_row0 = band * p.tr * 16u;
     const uint32_t tile_row0 = band_row0 + ti * 16u;
     const uint32_t nG = p.cols / GROUP;
     const uint32_t Gp = p.gp;
-    // The split's entries, tiles, groups and columns.
-    const uint32_t SE0 = split_begin(split, p.ns, p.n_entries);
-    const uint32_t SE1 = split_begin(split + 1, p.ns, p.n_entries);
+    // The split's entries (from the host: a uniform select, no division),
+    // tiles, groups and columns.
+    auto split_at = [&](uint32_t k) -> uint32_t {
+        return k == 0 ? p.split_e[0] : k == 1 ? p.split_e[1] : k == 2 ? p.split_e[2] : k == 3 ? p.split_e[3] : p.split_e[4];
+    };
+    const uint32_t SE0 = split_at(split);
+    const uint32_t SE1 = split_at(split + 1);
     const uint32_t ST0 = SE0 * TPE;
     const uint32_t ST1 = min(SE1 * TPE, p.tiles);
     const uint32_t nT = ST1 - ST0;
     const uint32_t G0 = ST0 * NGM;
     const uint32_t G1 = min(ST1 * NGM, nG);
-    // This wave's entries. The bounds are wave-uniform, but the split
-    // arithmetic above divides in 64 bits, which the compiler lowers to
-    // vector instructions: readfirstlane keeps them in scalar registers, so
-    // the entry offset below is a scalar soffset and not a per-lane value
+    // This wave's entries. The bounds are wave-uniform; readfirstlane keeps
+    // them in scalar registers whatever the compiler makes of the arithmetic,
+    // so the entry offset below is a scalar soffset and not a per-lane value
     // that would put every code load in a readfirstlane loop.
     const uint32_t nSE = SE1 - SE0;
-    const uint32_t E0 = __builtin_amdgcn_readfirstlane(SE0 + kw * nSE / KW);
-    const uint32_t E1 = __builtin_amdgcn_readfirstlane(SE0 + (kw + 1) * nSE / KW);
+    const uint32_t E0 = __builtin_amdgcn_readfirstlane(SE0 + ((kw * nSE) >> p.kw_shift));
+    const uint32_t E1 = __builtin_amdgcn_readfirstlane(SE0 + (((kw + 1) * nSE) >> p.kw_shift));
 
     uint32_t *ldsM = reinterpret_cast<uint32_t *>(lds);  // [tr*16][Gp] s|b<<16, or [tr*16][Gp][2] f32
     unsigned char *img = lds + p.meta_bytes;              // [nT] tile images
@@ -171,21 +170,25 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     // multiple of VEC); the `lead` groups before G0 and those past G1 are
     // read and dropped, so splits may start at any entry. Rows past the
     // matrix read zeros through the buffer range check. ----
+    // Thread tid loads column tid % 2^unit_shift of rows tid >> unit_shift,
+    // + rstep, ... (2^unit_shift >= units per row: no division, and
+    // consecutive lanes read consecutive 16 bytes of a row).
     const bool vec_meta = (nG * MB) % 16 == 0;
     const uint32_t lead = G0 % uint32_t(VEC);
     const uint32_t Ga = G0 - lead;
     const uint32_t Gb = (G1 + uint32_t(VEC) - 1) / uint32_t(VEC) * uint32_t(VEC);
     const uint32_t upr = vec_meta ? (Gb - Ga) / uint32_t(VEC) : 0u;  // units per row
-    const uint32_t units = p.tr * 16u * upr;
-    auto unit_off = [&](uint32_t f) -> uint32_t {
-        const uint32_t rl = f / upr;
-        return ((band_row0 + rl) * nG + Ga) * MB + (f - rl * upr) * 16u;
-    };
+    const uint32_t band_rows = p.tr * 16u;
+    const uint32_t ucol = uint32_t(tid) & ((1u << p.unit_shift) - 1u);
+    const uint32_t urow = uint32_t(tid) >> p.unit_shift;
+    const uint32_t rstep = uint32_t(nthr) >> p.unit_shift;
+    const bool ucol_ok = ucol < upr;
+    auto unit_off = [&](uint32_t rl) -> uint32_t { return ((band_row0 + rl) * nG + Ga) * MB + ucol * 16u; };
     u4 ms[kMetaUnits], mbv[kMetaUnits];
 #pragma unroll
     for (int u = 0; u < kMetaUnits; ++u) {
-        const uint32_t f = uint32_t(tid) + uint32_t(u * nthr);
-        const uint32_t off = f < units ? unit_off(f) : kOut;
+        const uint32_t rl = urow + uint32_t(u) * rstep;
+        const uint32_t off = (ucol_ok && rl < band_rows) ? unit_off(rl) : kOut;
         ms[u] = __builtin_amdgcn_raw_buffer_load_b128(sr, int(off), 0, 0);
         mbv[u] = __builtin_amdgcn_raw_buffer_load_b128(br, int(off), 0, 0);
     }
@@ -241,13 +244,14 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     }
     // ---- 5. Metadata to LDS. ----
     if (vec_meta) {
-        // Unit f holds groups g .. g+VEC-1 of its row (g relative to G0, so
-        // negative in the lead); only groups in [0, G1 - G0) are kept.
+        // This thread's units hold groups g .. g+VEC-1 of their rows (g
+        // relative to G0: negative in the lead); only groups in [0, G1 - G0)
+        // are kept, which checks only a row's first and last unit.
         const uint32_t ng = G1 - G0;
-        auto put = [&](uint32_t f, const u4 &sv, const u4 &bv) {
-            const uint32_t rl = f / upr;
-            const int g = int((f - rl * upr) * uint32_t(VEC)) - int(lead);
-            auto keep = [&](int gg) { return gg >= 0 && uint32_t(gg) < ng; };
+        const int g = int(ucol * uint32_t(VEC)) - int(lead);
+        const bool inner = ucol > 0 && ucol + 1 < upr;
+        auto put = [&](uint32_t rl, const u4 &sv, const u4 &bv) {
+            auto keep = [&](int gg) { return inner || (gg >= 0 && uint32_t(gg) < ng); };
             if constexpr (META == 0) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -266,16 +270,18 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
                 }
             }
         };
+        if (ucol_ok) {
 #pragma unroll
-        for (int u = 0; u < kMetaUnits; ++u) {
-            const uint32_t f = uint32_t(tid) + uint32_t(u * nthr);
-            if (f < units) put(f, ms[u], mbv[u]);
-        }
-        // Workgroups with more runs than the unrolled loads read the rest here.
-        for (uint32_t f = uint32_t(tid) + uint32_t(kMetaUnits * nthr); f < units; f += uint32_t(nthr)) {
-            const uint32_t off = unit_off(f);
-            put(f, __builtin_amdgcn_raw_buffer_load_b128(sr, int(off), 0, 0),
-                __builtin_amdgcn_raw_buffer_load_b128(br, int(off), 0, 0));
+            for (int u = 0; u < kMetaUnits; ++u) {
+                const uint32_t rl = urow + uint32_t(u) * rstep;
+                if (rl < band_rows) put(rl, ms[u], mbv[u]);
+            }
+            // Bands with more rows than the unrolled loads cover read the rest here.
+            for (uint32_t rl = urow + uint32_t(kMetaUnits) * rstep; rl < band_rows; rl += rstep) {
+                const uint32_t off = unit_off(rl);
+                put(rl, __builtin_amdgcn_raw_buffer_load_b128(sr, int(off), 0, 0),
+                    __builtin_amdgcn_raw_buffer_load_b128(br, int(off), 0, 0));
+            }
         }
     } else {
         const uint32_t ng = G1 - G0;
@@ -484,9 +490,35 @@ hipError_t launch_meta(const BandParams &p, const TilePlan &pl, uint32_t group, 
     }
 }
 
+// First entry of split s (the last split ends at n_entries): splits differ
+// by at most one entry.
 uint32_t host_split_begin(uint32_t s, uint32_t ns, uint32_t n_entries) {
     if (s >= ns) return n_entries;
     return uint32_t((uint64_t(s) * n_entries) / ns);
+}
+
+// log2 of the smallest power of two >= the 16-byte metadata units of any
+// split's row run (the kernel's Ga..Gb), as the kernel computes them.
+uint32_t meta_unit_shift(const AffineArgs &a, uint32_t ns, uint32_t n_entries) {
+    const uint32_t tpe = 8 / a.bits, ngm = kTileK / a.group;
+    const uint32_t tiles = (a.cols + kTileK - 1) / kTileK, ng = a.cols / a.group;
+    const uint32_t vec = a.meta == Meta::F32 ? 4 : 8;
+    uint32_t most = 1;
+    for (uint32_t sp = 0; sp < ns; ++sp) {
+        const uint32_t g0 = host_split_begin(sp, ns, n_entries) * tpe * ngm;
+        const uint32_t g1 = std::min(std::min(host_split_begin(sp + 1, ns, n_entries) * tpe, tiles) * ngm, ng);
+        const uint32_t ga = g0 - g0 % vec, gb = (g1 + vec - 1) / vec * vec;
+        most = std::max(most, (gb - ga) / vec);
+    }
+    uint32_t shift = 0;
+    while ((1u << shift) < most) ++shift;
+    return shift;
+}
+
+uint32_t log2_exact(uint32_t v) {
+    uint32_t k = 0;
+    while ((1u << k) < v) ++k;
+    return k;
 }
 
 // The plain form's kernel instance for a format, x-item count and ring
@@ -632,6 +664,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                     if (force_kw && kw != force_kw) continue;
                     const uint32_t threads = tr * kw * 64;
                     if (threads > uint32_t(kMaxThreads) || kw > max_se) continue;
+                    if ((1u << meta_unit_shift(a, ns, n_entries)) > threads) continue;
                     const uint32_t items = max_tiles * a.batch * 16;
                     const uint32_t xi = (items + threads - 1) / threads;
                     if (xi > 8) continue;
@@ -704,6 +737,9 @@ hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned 
     p.gp = pl.gp;
     p.meta_bytes = pl.meta_bytes;
     p.img_bytes = pl.img_bytes;
+    for (uint32_t k = 0; k < 5; ++k) p.split_e[k] = host_split_begin(k, pl.ns, pl.n_entries);
+    p.kw_shift = log2_exact(pl.kw);
+    p.unit_shift = meta_unit_shift(a, pl.ns, pl.n_entries);
     const int meta = static_cast<int>(a.meta);
     if (a.bits == 4) {
         if (meta == 0) return launch_meta<4, 0>(p, pl, a.group, a.batch, stream);
