@@ -44,6 +44,11 @@ under "dense_f16".
 The checkpoint loader (MLX safetensors to device buffers) is timed on one
 layer's three MLP matrices and reported under "loader" (host-to-device GB/s).
 
+The reference's shared-weight block microbenchmark (B GEMVs in one command
+against one block dispatch, alternating AB/BA, medians of the frame GPU
+time) runs at the metric shape with B=3 and is reported under
+"block_vs_sequential".
+
 BASELINE config 4 (the wide block: 17408x5120 Q4/g64 BF16 times 128 and 256
 FP32 columns) is timed the same way and reported under "wide" with its own
 matrix-core roofline (algorithmic FLOP against the dense f16 peak); it is not
@@ -491,6 +496,78 @@ def hip_kernel(plan) -> str:
             -3: "affine_rows_kernel"}.get(plan[0], "affine_gemv_kernel")
 
 
+def bench_block_vs_sequential(gpu: qmr.Gpu, iterations: int) -> dict:
+    """The reference's shared-weight block microbenchmark
+    (examples/block_matrix_bench.rs:28-172) at the metric shape with B=3: one
+    command holding B separate GEMVs (matvec_affine_bf16 at x/y offsets of
+    token t) against one command holding the block (matmul_affine_bf16),
+    same weights, inputs and output buffer, five warmups per mode, then
+    `iterations` of each in alternating AB/BA order; medians of the
+    command's FrameTiming GPU time and of its wall time. The data is the
+    reference benchmark's synthetic pattern. The two results must agree
+    within the reference's bound (1e-3 + 5e-5*|y|). One weight copy, as in
+    the reference: its 50 MB may be served from the Infinity Cache."""
+    rows, cols, batch = 5120, 17408, 3
+    total = rows * cols
+    i = np.arange(total // 8, dtype=np.uint64)
+    w = ((i * 0x9E3779B9 + 0x1478ABCF) & 0xFFFFFFFF).astype(np.uint32)
+    g = np.arange(total // 64)
+    scales = ((1 + g % 11) / 512.0).astype(np.float32)
+    biases = ((g % 9) / 256.0 - 0.0625).astype(np.float32)
+    inputs = ((np.arange(batch * cols) * 13 % 101 - 50) / 50.0).astype(np.float32)
+    bf16 = lambda v: (v.view(np.uint32) >> 16).astype(np.uint16)
+    bufs = [gpu.upload_bytes(w), gpu.upload_bytes(bf16(scales)), gpu.upload_bytes(bf16(biases)),
+            gpu.upload_f32(inputs), gpu.alloc_f32(batch * rows)]
+    log(f"bench: block vs sequential, {rows}x{cols} B={batch} ({iterations} per mode, AB/BA)")
+
+    def measure(block: bool):
+        t0 = time.perf_counter()
+        cmd = gpu.begin()
+        if block:
+            cmd.encode("matmul_affine_bf16", bufs, [rows, cols, 4, 64, batch], rows * 32, 128)
+        else:
+            for t in range(batch):
+                cmd.encode("matvec_affine_bf16", bufs, [rows, cols, 4, 64], rows * 32, 128,
+                           offsets=[0, 0, 0, t * cols * 4, t * rows * 4])
+        timing = cmd.finish()
+        cmd.release()
+        return timing.gpu_seconds, time.perf_counter() - t0
+
+    for _ in range(5):
+        measure(False)
+        measure(True)
+    times = {False: ([], []), True: ([], [])}
+    for it in range(iterations):
+        for block in (it % 2 == 0, it % 2 != 0):
+            g_s, w_s = measure(block)
+            times[block][0].append(g_s)
+            times[block][1].append(w_s)
+    measure(False)
+    expected = gpu.read_f32(bufs[4], batch * rows)
+    measure(True)
+    actual = gpu.read_f32(bufs[4], batch * rows)
+    diff = np.abs(actual.astype(np.float64) - expected)
+    ok = bool(np.isfinite(actual).all() and (diff <= 1e-3 + np.abs(expected) * 5e-5).all())
+    med = lambda v: float(statistics.median(v))
+    r = {
+        "kind": "shared_weight_matrix_block_microbenchmark",
+        "rows": rows, "cols": cols, "batch": batch, "bits": 4, "group_size": 64, "metadata_mode": "bf16",
+        "iterations_per_mode": iterations,
+        "sequential_gpu_median_ms": round(med(times[False][0]) * 1e3, 4),
+        "block_gpu_median_ms": round(med(times[True][0]) * 1e3, 4),
+        "gpu_speedup": round(med(times[False][0]) / med(times[True][0]), 3),
+        "sequential_wall_median_ms": round(med(times[False][1]) * 1e3, 4),
+        "block_wall_median_ms": round(med(times[True][1]) * 1e3, 4),
+        "max_absolute_difference": float(diff.max()),
+        "within_reference_bound": ok,
+    }
+    log(f"bench:   sequential {r['sequential_gpu_median_ms']} ms, block {r['block_gpu_median_ms']} ms GPU "
+        f"(speedup {r['gpu_speedup']}), max |diff| {r['max_absolute_difference']:.3g}")
+    if not ok:
+        raise AssertionError("block/GEMV mismatch beyond 1e-3 + 5e-5*|y|")
+    return r
+
+
 def read_floor(gpu: qmr.Gpu, m: synth.PackedMatrix, mats, args, steps: int = 0) -> dict:
     """The streaming-read floor of the metric launch: read_checksum (16-byte
     non-temporal loads over contiguous per-workgroup slices, XOR-reduced into
@@ -552,6 +629,8 @@ def main() -> int:
     ap.add_argument("--no-mlp", action="store_true", help="skip the fused decoder-MLP timing")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense F16 timing")
     ap.add_argument("--no-loader", action="store_true", help="skip the checkpoint-loader timing")
+    ap.add_argument("--block-iters", type=int, default=100,
+                    help="iterations per mode of the block vs sequential comparison (0 skips it)")
     ap.add_argument("--no-config3", action="store_true",
                     help="skip the config-3 Q8 projection and vocabulary head")
     ap.add_argument("--gemv-plan", default=None, metavar="RR,KS",
@@ -633,6 +712,7 @@ def main() -> int:
     mlp = [] if (args.only_metric or args.no_mlp) else bench_mlp(gpu, args)
     dense = [] if (args.only_metric or args.no_dense) else bench_dense(gpu, args)
     loader = None if (args.only_metric or args.no_loader) else bench_loader(args)
+    block_seq = None if (args.only_metric or args.block_iters <= 0) else bench_block_vs_sequential(gpu, args.block_iters)
     head = next(r for r in results if r["tag"] == "down" and r["batch"] == 1)
     b3 = next(r for r in results if r["tag"] == "down" and r["batch"] == 3)
     cpu = None
@@ -687,6 +767,7 @@ def main() -> int:
         "dense_f16": dense,
         "loader": loader,
         "wide": wide,
+        "block_vs_sequential": block_seq,
     }
     print(json.dumps(line), flush=True)
     gpu.close()
