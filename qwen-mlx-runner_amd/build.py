@@ -24,7 +24,15 @@ ARCH = os.environ.get("QMR_OFFLOAD_ARCH", "gfx950")
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", f"--offload-arch={ARCH}"]
 
+# The band kernel's source compiles once per weight format (bits x scale
+# type), each object holding that format's instances, plus once without the
+# format macros for its planner; these are the longest compiles, so they are
+# queued first.
+BAND_FORMATS = [(bits, meta) for bits in (4, 8) for meta in (0, 1, 2)]
+
 SOURCES = [
+    *[("affine_tile.hip", ["-x", "hip", f"-DQMR_BAND_BITS={bits}", f"-DQMR_BAND_META={meta}"],
+       f"affine_tile_q{bits}_m{meta}.o") for bits, meta in BAND_FORMATS],
     ("contract.cpp", ["-x", "c++"]),
     ("checkpoint.cpp", ["-x", "c++"]),
     ("runtime.cpp", ["-x", "hip"]),
@@ -46,8 +54,8 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (expected /opt/rocm/bin/hipcc)")
 
 
-def _compile(src: str, lang: list[str]) -> Path:
-    obj = BUILD / (src + ".o")
+def _compile(src: str, lang: list[str], obj_name: str | None = None) -> Path:
+    obj = BUILD / (obj_name or src + ".o")
     cmd = [hipcc(), *COMMON, *lang, "-c", str(CSRC / src), "-o", str(obj)]
     if lang[:2] == ["-x", "hip"]:
         cmd[1:1] = DEVICE_FLAGS

@@ -38,6 +38,12 @@
 // counter and no fence chain. The sum is taken in split order, so results
 // do not depend on timing. The wait is bounded: past the host's spin limit
 // the workgroup writes NaN and exits, so every wave always finishes.
+//
+// Build. This file is compiled once per weight format with
+// -DQMR_BAND_BITS=<4|8> -DQMR_BAND_META=<0|1|2>: each such object holds the
+// kernel instances of that format (launch_meta, instance_meta), and the
+// objects compile in parallel. Compiled without them it holds the planner
+// and the launch entry, which call those two through their declarations.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -51,9 +57,7 @@
 #include "mfma_common.hpp"
 
 namespace qmr {
-namespace {
-
-using namespace mfma;
+namespace band {
 
 constexpr int kMaxThreads = 512;  // up to 8 waves: x staging needs up to 8 items of registers per thread
 constexpr int kMetaUnits = 4;  // 16-byte metadata loads per thread and plane (fast path)
@@ -65,7 +69,14 @@ struct BandParams {
     const float *x;
     float *y;
     const float *r;              // residual added in the final store (may alias y), or null
-    unsigned long long *partial;  // [ns-1][B][rows] {value, epoch} slots (ns > 1)
+    // Fused MLP form: the up matrix (same shape and format as w/s/b, the
+    // gate), the RMS-norm weights [cols] and epsilon.
+    const uint32_t *w2;
+    const void *s2;
+    const void *b2;
+    const float *norm;
+    float eps;
+    unsigned long long *partial;  // {value, epoch} slots: [ns-1][B][rows], or [2*ns][B][rows] for the MLP form
     uint32_t epoch;
     uint32_t spin_limit;
     uint32_t rows, cols;
@@ -81,6 +92,27 @@ struct BandParams {
     uint32_t unit_shift;  // log2 of the threads per row in the metadata loads (>= units per row)
 };
 
+// Launches the plan's instance of format <BITS, META> (META 0 f16, 1 bf16,
+// 2 f32 scales and biases) for a group size and batch.
+template <int BITS, int META>
+hipError_t launch_meta(const BandParams &p, const TilePlan &pl, uint32_t group, uint32_t batch, hipStream_t stream);
+
+// The kernel instance for a format, x-item count, ring depth and form
+// (plain or the MLP form; the residual form's resources are the plain's),
+// for occupancy queries; null for a batch the group size does not allow.
+template <int BITS, int META>
+const void *instance_meta(uint32_t group, uint32_t batch, uint32_t xi, uint32_t ring, bool mlp);
+
+}  // namespace band
+
+#ifdef QMR_BAND_BITS
+namespace {
+
+using namespace mfma;
+using band::BandParams;
+using band::kMaxThreads;
+using band::kMetaUnits;
+
 template <int BITS, int GROUP, int B>
 constexpr uint32_t tile_img_bytes() {
     constexpr int NGM = kTileK / GROUP;
@@ -88,9 +120,16 @@ constexpr uint32_t tile_img_bytes() {
     return 4u * 4 * 2 * B * 16 + uint32_t(NGM) * (HALF / 2) * 16;
 }
 
-// XI: x items (8 columns each) staged per thread.
-template <int BITS, int META, int GROUP, int B, int XI, int P, bool RESID>
+// XI: x items (8 columns each) staged per thread. FUSE 0: y = W x; 1: y =
+// r + W x; 2: the fused MLP form, y = silu(G x^) * (U x^) with x^ =
+// rms_norm(x) * norm: the grid holds the gate's bands and splits, then the
+// up matrix's; x is staged times the norm weights, every workgroup but the
+// up matrix's last split of a band publishes its sums, and that one adds
+// the gate's and up's sums in split order and applies 1/rms (the products
+// are linear in it) and SwiGLU.
+template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE>
 __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) {
+    constexpr bool MLP = FUSE == 2;
     constexpr int NGM = kTileK / GROUP;  // quant groups per tile
     constexpr int SLOTS = 16 / NGM;      // A rows per quant group
     constexpr int HALF = SLOTS / 2;      // RHS per quant group in D (>= B)
@@ -112,8 +151,13 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const uint32_t KW = p.kw;
     const uint32_t ti = uint32_t(wave) >> p.kw_shift;
     const uint32_t kw = uint32_t(wave) & (KW - 1u);
-    const uint32_t band = blockIdx.x % p.nbands;
-    const uint32_t split = blockIdx.x / p.nbands;
+    const uint32_t per_mat = p.nbands * p.ns;
+    const uint32_t mat = MLP ? blockIdx.x / per_mat : 0u;  // 0: w/s/b (the gate), 1: the up matrix
+    const uint32_t bid = blockIdx.x - mat * per_mat;
+    const uint32_t band = bid % p.nbands;
+    const uint32_t split = bid / p.nbands;
+    // The MLP form's finishing workgroups: the up matrix's last split.
+    const bool finisher = MLP && mat == 1 && split + 1 == p.ns;
     const uint32_t band_row0 = band * p.tr * 16u;
     const uint32_t tile_row0 = band_row0 + ti * 16u;
     const uint32_t nG = p.cols / GROUP;
@@ -141,13 +185,17 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     uint32_t *ldsM = reinterpret_cast<uint32_t *>(lds);  // [tr*16][Gp] s|b<<16, or [tr*16][Gp][2] f32
     unsigned char *img = lds + p.meta_bytes;              // [nT] tile images
     float *red = reinterpret_cast<float *>(lds + p.meta_bytes + p.img_bytes);
+    float *sq = red + p.tr * KW * B * 16u;  // MLP: [wave][B] partial sums of x^2 (finishers)
 
+    const uint32_t *wp = MLP && mat ? p.w2 : p.w;
+    const void *sp_ = MLP && mat ? p.s2 : p.s;
+    const void *bp = MLP && mat ? p.b2 : p.b;
     const __amdgpu_buffer_rsrc_t wr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(p.w), 0, int(p.w_bytes), kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(wp), 0, int(p.w_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.s), 0, int(p.m_bytes), kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(sp_), 0, int(p.m_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t br =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.b), 0, int(p.m_bytes), kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(bp), 0, int(p.m_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(p.x), 0, int(uint32_t(B) * p.cols * 4u), kRsrcWord3);
 
@@ -161,6 +209,32 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     for (int i = 0; i < XI; ++i) {
         const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
         load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), ST0 * kTileK + item_col<B>(it), p.cols, it < items);
+    }
+    // MLP: the norm weights of the same columns, and in the finishers each
+    // x[t]'s sum of squares over all columns (for 1/rms at the end).
+    [[maybe_unused]] float nv[MLP ? XI : 1][8];
+    if constexpr (MLP) {
+        const __amdgpu_buffer_rsrc_t nr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p.norm), 0, int(p.cols * 4u), kRsrcWord3);
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
+            load_x8(nv[i], nr, 0u, ST0 * kTileK + item_col<B>(it), p.cols, it < items);
+        }
+        if (finisher) {
+#pragma unroll
+            for (int t = 0; t < B; ++t) {
+                float v = 0.f;
+                for (uint32_t k = uint32_t(tid) * 4u; k < p.cols; k += uint32_t(nthr) * 4u) {
+                    const u4 q = __builtin_amdgcn_raw_buffer_load_b128(xr, int((uint32_t(t) * p.cols + k) * 4u), 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v += __uint_as_float(q[e]) * __uint_as_float(q[e]);
+                }
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+                if (lane == 0) sq[wave * B + t] = v;
+            }
+        }
     }
 
     // ---- 2. Metadata of the band's rows over the split's groups: one run
@@ -240,6 +314,10 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     for (int i = 0; i < XI; ++i) {
         const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
         if (i > 0 && uint32_t(tid) - uint32_t(lane) + uint32_t(i * nthr) >= items) break;  // whole waves in or out
+        if constexpr (MLP) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xv[i][j] *= nv[i][j];
+        }
         stage_x_item<BITS, GROUP, B>(xv[i], it, it < items, lane, imgA, imgS);
     }
     // ---- 5. Metadata to LDS. ----
@@ -391,40 +469,67 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     float v = src[0];
     for (uint32_t k = 1; k < KW; ++k) v += src[size_t(k) * B * 16u];
     const size_t oy = size_t(t) * p.rows + row;
-    if (p.ns > 1) {
-        const size_t slot = oy;  // [split][B][rows]
-        const size_t stride = size_t(B) * p.rows;
-        if (split + 1 < p.ns) {
-            const unsigned long long word = (static_cast<unsigned long long>(p.epoch) << 32) | __float_as_uint(v);
-            __hip_atomic_store(p.partial + size_t(split) * stride + slot, word, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+    const size_t stride = size_t(B) * p.rows;
+    // Reads slot set k's value for oy once its epoch is this launch's;
+    // past the host's spin limit it gives up (the caller writes NaN).
+    auto take = [&](uint32_t k, bool &ok) -> float {
+        unsigned long long *q = p.partial + size_t(k) * stride + oy;
+        unsigned long long word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (uint32_t spin = 0; uint32_t(word >> 32) != p.epoch; ++spin) {
+            if (spin >= p.spin_limit) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return __uint_as_float(uint32_t(word));
+    };
+    auto publish = [&](uint32_t k) {
+        const unsigned long long word = (static_cast<unsigned long long>(p.epoch) << 32) | __float_as_uint(v);
+        __hip_atomic_store(p.partial + size_t(k) * stride + oy, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    if constexpr (MLP) {
+        // Slot sets [mat*ns + split]. The finisher adds the gate's splits and
+        // then the up matrix's, in split order.
+        if (!finisher) {
+            publish(mat * p.ns + split);
             return;
         }
-        // The band's last split: the other splits' sums, in split order.
-        float sum = 0.f;
         bool ok = true;
-        for (uint32_t k = 0; k + 1 < p.ns; ++k) {
-            unsigned long long *q = p.partial + size_t(k) * stride + slot;
-            unsigned long long word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            for (uint32_t spin = 0; uint32_t(word >> 32) != p.epoch; ++spin) {
-                if (spin >= p.spin_limit) {
-                    ok = false;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-                word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            const float pv = __uint_as_float(uint32_t(word));
-            sum = k == 0 ? pv : sum + pv;
+        float g = take(0, ok);
+        for (uint32_t k = 1; k < p.ns; ++k) g += take(k, ok);
+        float u = v;
+        if (p.ns > 1) {
+            float su = take(p.ns, ok);
+            for (uint32_t k = 1; k + 1 < p.ns; ++k) su += take(p.ns + k, ok);
+            u = su + v;
         }
-        v = ok ? sum + v : __builtin_nanf("");
+        float ss = 0.f;
+        for (uint32_t wv = 0; wv < p.tr * KW; ++wv) ss += sq[wv * B + t];
+        const float inv = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
+        const float gn = g * inv;
+        p.y[oy] = ok ? gn * (1.0f / (1.0f + expf(-gn))) * (u * inv) : __builtin_nanf("");
+        return;
+    } else {
+        if (p.ns > 1) {
+            if (split + 1 < p.ns) {
+                publish(split);
+                return;
+            }
+            // The band's last split: the other splits' sums, in split order.
+            bool ok = true;
+            float sum = take(0, ok);
+            for (uint32_t k = 1; k + 1 < p.ns; ++k) sum += take(k, ok);
+            v = ok ? sum + v : __builtin_nanf("");
+        }
+        p.y[oy] = FUSE == 1 ? p.r[oy] + v : v;
     }
-    p.y[oy] = RESID ? p.r[oy] + v : v;
 }
 
-template <int BITS, int META, int GROUP, int B, int XI, int P, bool RESID>
+template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE>
 hipError_t launch_inst(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
-    auto kernel = affine_band_kernel<BITS, META, GROUP, B, XI, P, RESID>;
+    auto kernel = affine_band_kernel<BITS, META, GROUP, B, XI, P, FUSE>;
     static size_t configured = 0;
     if (pl.lds > 65536 && pl.lds > configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
@@ -432,18 +537,22 @@ hipError_t launch_inst(const BandParams &p, const TilePlan &pl, hipStream_t stre
         if (e != hipSuccess) return e;
         configured = pl.lds;
     }
-    hipLaunchKernelGGL(kernel, dim3(pl.nbands * pl.ns), dim3(pl.tr * pl.kw * 64), pl.lds, stream, p);
+    const uint32_t mats = FUSE == 2 ? 2u : 1u;
+    hipLaunchKernelGGL(kernel, dim3(mats * pl.nbands * pl.ns), dim3(pl.tr * pl.kw * 64), pl.lds, stream, p);
     return hipGetLastError();
 }
 
 template <int BITS, int META, int GROUP, int B, int XI>
 hipError_t launch_xi(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
-    const bool resid = p.r != nullptr;
-    if (pl.ring >= 3)
-        return resid ? launch_inst<BITS, META, GROUP, B, XI, 3, true>(p, pl, stream)
-                     : launch_inst<BITS, META, GROUP, B, XI, 3, false>(p, pl, stream);
-    return resid ? launch_inst<BITS, META, GROUP, B, XI, 2, true>(p, pl, stream)
-                 : launch_inst<BITS, META, GROUP, B, XI, 2, false>(p, pl, stream);
+    const int fuse = p.w2 != nullptr ? 2 : p.r != nullptr ? 1 : 0;
+    if (pl.ring >= 3) {
+        if (fuse == 2) return launch_inst<BITS, META, GROUP, B, XI, 3, 2>(p, pl, stream);
+        return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 3, 1>(p, pl, stream)
+                         : launch_inst<BITS, META, GROUP, B, XI, 3, 0>(p, pl, stream);
+    }
+    if (fuse == 2) return launch_inst<BITS, META, GROUP, B, XI, 2, 2>(p, pl, stream);
+    return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 2, 1>(p, pl, stream)
+                     : launch_inst<BITS, META, GROUP, B, XI, 2, 0>(p, pl, stream);
 }
 
 // x items per thread: the smallest compiled count that covers the plan's.
@@ -479,6 +588,44 @@ hipError_t launch_group(const BandParams &p, const TilePlan &pl, uint32_t batch,
     return hipErrorInvalidValue;
 }
 
+template <int BITS, int META, int GROUP>
+const void *instance_group(uint32_t batch, uint32_t xi, uint32_t ring, bool mlp) {
+    constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
+    auto pick = [&](auto bconst) -> const void * {
+        constexpr int B = decltype(bconst)::value;
+        auto by_ring = [&](auto xconst) -> const void * {
+            constexpr int XI = decltype(xconst)::value;
+            if (mlp)
+                return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, 2>)
+                                 : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, 2>);
+            return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, 0>)
+                             : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, 0>);
+        };
+        switch (xi_instance(xi)) {
+            case 2: return by_ring(std::integral_constant<int, 2>{});
+            case 4: return by_ring(std::integral_constant<int, 4>{});
+            case 5: return by_ring(std::integral_constant<int, 5>{});
+            default: return by_ring(std::integral_constant<int, 8>{});
+        }
+    };
+    switch (batch) {
+        case 1: return pick(std::integral_constant<int, 1>{});
+        case 2: return pick(std::integral_constant<int, 2>{});
+        case 3:
+            if constexpr (MAXB >= 3) return pick(std::integral_constant<int, 3>{});
+            break;
+        case 4:
+            if constexpr (MAXB >= 4) return pick(std::integral_constant<int, 4>{});
+            break;
+        default: break;
+    }
+    return nullptr;
+}
+
+}  // namespace
+
+namespace band {
+
 template <int BITS, int META>
 hipError_t launch_meta(const BandParams &p, const TilePlan &pl, uint32_t group, uint32_t batch,
                        hipStream_t stream) {
@@ -489,6 +636,31 @@ hipError_t launch_meta(const BandParams &p, const TilePlan &pl, uint32_t group, 
         default: return hipErrorInvalidValue;
     }
 }
+
+template <int BITS, int META>
+const void *instance_meta(uint32_t group, uint32_t batch, uint32_t xi, uint32_t ring, bool mlp) {
+    switch (group) {
+        case 32: return instance_group<BITS, META, 32>(batch, xi, ring, mlp);
+        case 64: return instance_group<BITS, META, 64>(batch, xi, ring, mlp);
+        case 128: return instance_group<BITS, META, 128>(batch, xi, ring, mlp);
+        default: return nullptr;
+    }
+}
+
+template hipError_t launch_meta<QMR_BAND_BITS, QMR_BAND_META>(const BandParams &, const TilePlan &, uint32_t, uint32_t,
+                                                               hipStream_t);
+template const void *instance_meta<QMR_BAND_BITS, QMR_BAND_META>(uint32_t, uint32_t, uint32_t, uint32_t, bool);
+
+}  // namespace band
+
+#else  // the planner and the launch entry
+namespace {
+
+using namespace mfma;
+using band::BandParams;
+using band::instance_meta;
+using band::kMaxThreads;
+using band::launch_meta;
 
 // First entry of split s (the last split ends at n_entries): splits differ
 // by at most one entry.
@@ -521,59 +693,17 @@ uint32_t log2_exact(uint32_t v) {
     return k;
 }
 
-// The plain form's kernel instance for a format, x-item count and ring
-// depth, for occupancy queries.
-template <int BITS, int META, int GROUP>
-const void *instance_group(uint32_t batch, uint32_t xi, uint32_t ring) {
-    constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
-    auto pick = [&](auto bconst) -> const void * {
-        constexpr int B = decltype(bconst)::value;
-        auto by_ring = [&](auto xconst) -> const void * {
-            constexpr int XI = decltype(xconst)::value;
-            return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, false>)
-                             : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, false>);
-        };
-        switch (xi_instance(xi)) {
-            case 2: return by_ring(std::integral_constant<int, 2>{});
-            case 4: return by_ring(std::integral_constant<int, 4>{});
-            case 5: return by_ring(std::integral_constant<int, 5>{});
-            default: return by_ring(std::integral_constant<int, 8>{});
-        }
-    };
-    switch (batch) {
-        case 1: return pick(std::integral_constant<int, 1>{});
-        case 2: return pick(std::integral_constant<int, 2>{});
-        case 3:
-            if constexpr (MAXB >= 3) return pick(std::integral_constant<int, 3>{});
-            break;
-        case 4:
-            if constexpr (MAXB >= 4) return pick(std::integral_constant<int, 4>{});
-            break;
-        default: break;
-    }
-    return nullptr;
-}
-
-template <int BITS, int META>
-const void *instance_meta(uint32_t group, uint32_t batch, uint32_t xi, uint32_t ring) {
-    switch (group) {
-        case 32: return instance_group<BITS, META, 32>(batch, xi, ring);
-        case 64: return instance_group<BITS, META, 64>(batch, xi, ring);
-        case 128: return instance_group<BITS, META, 128>(batch, xi, ring);
-        default: return nullptr;
-    }
-}
-
 const void *instance(const AffineArgs &a, uint32_t xi, uint32_t ring) {
     const int meta = static_cast<int>(a.meta);
+    const bool mlp = a.up_w != nullptr;
     if (a.bits == 4) {
-        if (meta == 0) return instance_meta<4, 0>(a.group, a.batch, xi, ring);
-        if (meta == 1) return instance_meta<4, 1>(a.group, a.batch, xi, ring);
-        return instance_meta<4, 2>(a.group, a.batch, xi, ring);
+        if (meta == 0) return instance_meta<4, 0>(a.group, a.batch, xi, ring, mlp);
+        if (meta == 1) return instance_meta<4, 1>(a.group, a.batch, xi, ring, mlp);
+        return instance_meta<4, 2>(a.group, a.batch, xi, ring, mlp);
     }
-    if (meta == 0) return instance_meta<8, 0>(a.group, a.batch, xi, ring);
-    if (meta == 1) return instance_meta<8, 1>(a.group, a.batch, xi, ring);
-    return instance_meta<8, 2>(a.group, a.batch, xi, ring);
+    if (meta == 0) return instance_meta<8, 0>(a.group, a.batch, xi, ring, mlp);
+    if (meta == 1) return instance_meta<8, 1>(a.group, a.batch, xi, ring, mlp);
+    return instance_meta<8, 2>(a.group, a.batch, xi, ring, mlp);
 }
 
 // Resident workgroups per CU for an instance, block size and dynamic LDS,
@@ -601,7 +731,8 @@ uint32_t resident_per_cu(const void *kernel, uint32_t threads, size_t lds) {
 }  // namespace
 
 bool affine_tile_supported(const AffineArgs &a) {
-    if (a.up_w) return false;
+    if (a.up_w && (a.residual || a.norm == nullptr || !a.up_s || !a.up_b)) return false;
+    if (a.up_w && (reinterpret_cast<uintptr_t>(a.up_w) & 15) != 0) return false;
     if (a.bits != 4 && a.bits != 8) return false;
     if (a.group != 32 && a.group != 64 && a.group != 128) return false;
     const uint32_t maxb = (16 / (kTileK / a.group)) / 2;
@@ -625,6 +756,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     const uint32_t tiles = (a.cols + kTileK - 1) / kTileK;
     const uint32_t mb = a.meta == Meta::F32 ? 4 : 2;
     const uint32_t cus = lim.num_cus > 0 ? uint32_t(lim.num_cus) : 256u;
+    const bool mlp = a.up_w != nullptr;
     const size_t timg = size_t(4) * 4 * 2 * a.batch * 16 + size_t(ngm) * ((16 / ngm / 2) / 2) * 16;
     const double wbytes = double(a.rows) * row_bytes + 2.0 * a.rows * (a.cols / a.group) * mb;
     // Candidates: ring depth, K splits, tiles per band, waves per tile. Every
@@ -671,16 +803,19 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                     const uint32_t gp = (max_tiles * ngm) | 1u;
                     const size_t meta = (size_t(tr) * 16 * gp * 4 * (a.meta == Meta::F32 ? 2 : 1) + 15) & ~size_t(15);
                     const size_t img = size_t(max_tiles) * timg;
-                    const size_t lds = meta + img + size_t(tr * kw) * a.batch * 16 * 4;
+                    // The MLP form: the finishers' sums of squares after the
+                    // reduction area, and a grid of both matrices.
+                    const size_t lds = meta + img + size_t(tr * kw) * a.batch * 16 * 4 +
+                                       (mlp ? size_t(tr * kw) * a.batch * 4 : 0);
                     if (lds > lim.max_lds_per_block) continue;
-                    const double wgs = double(nbands) * ns;
+                    const double wgs = double(nbands) * ns * (mlp ? 2 : 1);
                     const uint32_t resident = resident_per_cu(instance(a, xi, ring), threads, lds);
                     if (wgs > double(resident) * cus) continue;
                     const double waves = wgs * tr * kw;
                     const double per_cu = std::ceil(wgs / cus) / (wgs / cus);
                     double score = 0.5 * std::fabs(std::log2(waves / (2.0 * 4 * cus)));
                     score += std::log2(per_cu);
-                    score += double(nbands) * a.batch * a.cols * 4.0 / wbytes;
+                    score += double(nbands) * a.batch * a.cols * 4.0 / wbytes;  // per matrix
                     score += std::fabs(std::log2(waves / cus * ring * 2048.0 / 36864.0));
                     score += ring == 2 ? 0.1 : 0.0;
                     if (score < best - 1e-9) {
@@ -706,6 +841,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
 }
 
 size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a) {
+    if (a.up_w) return size_t(2) * pl.ns * a.batch * a.rows * sizeof(unsigned long long);
     if (pl.ns <= 1) return 0;
     return size_t(pl.ns - 1) * a.batch * a.rows * sizeof(unsigned long long);
 }
@@ -713,7 +849,7 @@ size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a) {
 hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial, uint32_t epoch,
                               hipStream_t stream) {
     if (pl.kw == 0) return hipErrorInvalidValue;
-    if (pl.ns > 1 && partial == nullptr) return hipErrorInvalidValue;
+    if ((pl.ns > 1 || a.up_w) && partial == nullptr) return hipErrorInvalidValue;
     BandParams p;
     p.w = a.w;
     p.s = a.s;
@@ -721,6 +857,11 @@ hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned 
     p.x = a.x;
     p.y = a.y;
     p.r = a.residual;
+    p.w2 = a.up_w;
+    p.s2 = a.up_s;
+    p.b2 = a.up_b;
+    p.norm = a.norm;
+    p.eps = a.eps;
     p.partial = partial;
     p.epoch = epoch;
     p.spin_limit = 1u << 22;
@@ -750,5 +891,7 @@ hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned 
     if (meta == 1) return launch_meta<8, 1>(p, pl, a.group, a.batch, stream);
     return launch_meta<8, 2>(p, pl, a.group, a.batch, stream);
 }
+
+#endif
 
 }  // namespace qmr

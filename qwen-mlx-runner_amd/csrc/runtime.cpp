@@ -334,7 +334,7 @@ qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a,
     const int ks = f.rr == -4 ? f.ks : 0;
     uint64_t key = (uint64_t(a.rows) << 32) | a.cols;
     key = key * 1000003u ^ (uint64_t(a.bits) << 24 | uint64_t(a.group) << 12 | uint64_t(a.batch) << 4 |
-                            uint64_t(static_cast<int>(a.meta)) << 1 | (a.residual ? 1u : 0u));
+                            uint64_t(static_cast<int>(a.meta)) << 2 | (a.up_w ? 2u : 0u) | (a.residual ? 1u : 0u));
     key = key * 1000003u ^ uint64_t(uint32_t(ks));
     key = key * 1000003u ^ uint64_t(static_cast<int>(sched));
     const auto it = dev->band_plans.find(key);
@@ -956,15 +956,23 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
                 std::memcpy(&a.eps, &params[5], 4);
                 ensure(qmr::affine_rows_supported(a), name + ": no fused kernel for this format",
                        QMR_ERR_UNSUPPORTED);
-                // The split-K kernel (measured at 17408x5120: 26.1 us at B=1
-                // and 30.4 at B=3 against 29.4 and 35.5 for the row-owning
-                // MLP mode, although both matrices' grid takes two rounds of
-                // resident workgroups); the row-owning kernel's MLP mode when
-                // the tuning hook asks for it (rr == -3, ks = j*10000 +
-                // rt*100 + kw) or split-K has no plan.
+                // The row-band kernel's MLP form where it has a one-round
+                // plan for both matrices' grid (or the tuning hook forces it,
+                // rr == -4); else the split-K kernel (measured at 17408x5120:
+                // 26.1 us at B=1 and 30.4 at B=3 against 29.4 and 35.5 for
+                // the row-owning MLP mode, although both matrices' grid takes
+                // two rounds of resident workgroups), also when the hook asks
+                // for it (rr == -2); the row-owning kernel's MLP mode when
+                // the hook asks for it (rr == -3, ks = j*10000 + rt*100 + kw)
+                // or split-K has no plan.
                 const qmr::GemvPlan f = dev->forced_plan;
-                const qmr::MfmaPlan mp = qmr::plan_affine_mfma(a, dev->limits);
-                if (f.rr != -3 && mp.rt > 0) {
+                qmr::TilePlan bp;
+                if ((f.rr == 0 || f.rr == -4) && qmr::affine_tile_supported(a)) bp = forced_tile_plan(dev, a);
+                const qmr::MfmaPlan mp = bp.kw > 0 ? qmr::MfmaPlan{} : qmr::plan_affine_mfma(a, dev->limits);
+                if (bp.kw > 0) {
+                    e = launch_band(dev, a, bp, fixed);
+                    dev->last_hip += " (MLP)";
+                } else if (f.rr != -3 && mp.rt > 0) {
                     dev->last_hip = "affine_mfma_kernel (MLP)";
                     e = launch_split_k(dev, a, mp, fixed);
                 } else {

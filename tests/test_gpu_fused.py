@@ -58,8 +58,9 @@ def _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind):
 ])
 @pytest.mark.parametrize("rr", [0, -2, -3])
 def test_mlp_gate_up_swiglu_matches_unfused_oracle(gpu, rr, rows, cols, bits, group, batch, kind):
-    """Default plan, the split-K kernel forced (rr -2) and the row-owning
-    kernel's MLP mode forced (rr -3)."""
+    """Default plan (the row-band kernel's MLP form where it has a one-round
+    plan for both matrices' grid), the split-K kernel forced (rr -2) and the
+    row-owning kernel's MLP mode forced (rr -3)."""
     rng = np.random.default_rng(rows + 7 * cols + batch)
     gate_m = _matrix(rng, rows, cols, bits, group, kind)
     up_m = _matrix(rng, rows, cols, bits, group, kind)
@@ -74,6 +75,25 @@ def test_mlp_gate_up_swiglu_matches_unfused_oracle(gpu, rr, rows, cols, bits, gr
         assert np.array_equal(again.view(np.uint32), got.view(np.uint32)), "launches differ"
     finally:
         gpu.set_gemv_plan(0, 0)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_mlp_default_is_the_band_kernel_at_the_27b_shape(gpu, batch):
+    """At the 27B gate/up shape and B=1 the fused form runs on the row-band
+    kernel (both matrices in one grid, the up matrix's last split
+    finishing). At B=3 both matrices' workgroups do not fit one round of
+    resident workgroups (their x images take 32-64 KB of LDS each), so the
+    split-K kernel runs it."""
+    rows, cols = 17408, 5120
+    rng = np.random.default_rng(batch)
+    gate_m = _matrix(rng, rows, cols, 4, 64, "bf16")
+    up_m = _matrix(rng, rows, cols, 4, 64, "bf16")
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, 4, 64, batch, "bf16")
+    kernel = gpu.last_hip_kernel()
+    want = "affine_band_kernel" if batch == 1 else "affine_mfma_kernel"
+    assert kernel.startswith(want) and kernel.endswith("(MLP)"), kernel
 
 
 def test_mlp_rms_statistic_covers_every_column_and_rhs(gpu):
