@@ -92,8 +92,8 @@ struct BandParams {
     uint32_t unit_shift;  // log2 of the threads per row in the metadata loads (>= units per row)
 };
 
-// Launches the plan's instance of format <BITS, META> (META 0 f16, 1 bf16,
-// 2 f32 scales and biases) for a group size and batch.
+// Launches the plan's instance of format <BITS, META> (META 0 f32, 1 bf16,
+// 2 f16 scales and biases) for a group size and batch.
 template <int BITS, int META>
 hipError_t launch_meta(const BandParams &p, const TilePlan &pl, uint32_t group, uint32_t batch, hipStream_t stream);
 
