@@ -772,66 +772,87 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     //     slows with less (latency not covered) and with more (at 5120x17408
     //     B=1: 12.2 us with 30 KB, 11.9 with 45, 12.3 with 60)
     //   + 0.1 for a two-entry ring.
+    // Where no plan fits one round (a 151936-row vocabulary head), a second
+    // pass takes single-split bands, whose workgroups never wait on each
+    // other, so any number of rounds is safe: the tallest band, one wave per
+    // tile, and the ring whose codes in flight per CU (resident waves x ring
+    // x 2 KB) come closest to 48 KB. The MLP form's finishers wait on other
+    // workgroups, so it has no such pass. Measured at 151936x5120 Q4/g64,
+    // two boxes: B=1 76.7-80.4 us (tr 8, kw 1, ring 2; two workgroups per
+    // CU) against 86.4-89.8 for the row-owning kernel and 80.9-81.9 with
+    // ring 3; B=3 95.0-96.7 (ring 3; one 106 KB workgroup per CU) against
+    // 95.1-97.0 and 98.8-99.2 with ring 2. Two or three splits over several
+    // rounds measured slower at both batches.
     double best = 1e30;
-    for (uint32_t ring : {2u, 3u}) {
-        if (force_ring && ring != force_ring) continue;
-        for (uint32_t ns = 1; ns <= 4; ++ns) {
-            if (force_ns && ns != force_ns) continue;
-            if (ns > n_entries) continue;
-            uint32_t max_se = 0;
-            bool empty = false;
-            for (uint32_t sp = 0; sp < ns; ++sp) {
-                const uint32_t e0 = host_split_begin(sp, ns, n_entries);
-                const uint32_t e1 = host_split_begin(sp + 1, ns, n_entries);
-                if (e1 <= e0) empty = true;
-                else max_se = std::max(max_se, e1 - e0);
-            }
-            if (empty) continue;
-            const uint32_t max_tiles = std::min(max_se * tpe, tiles);
-            for (uint32_t tr : {1u, 2u, 4u, 8u}) {
-                if (force_tr && tr != force_tr) continue;
-                if (tr > 1 && (tr / 2) * 16 >= a.rows) continue;
-                const uint32_t nbands = (row_tiles + tr - 1) / tr;
-                for (uint32_t kw : {1u, 2u, 4u, 8u}) {
-                    if (force_kw && kw != force_kw) continue;
-                    const uint32_t threads = tr * kw * 64;
-                    if (threads > uint32_t(kMaxThreads) || kw > max_se) continue;
-                    if ((1u << meta_unit_shift(a, ns, n_entries)) > threads) continue;
-                    const uint32_t items = max_tiles * a.batch * 16;
-                    const uint32_t xi = (items + threads - 1) / threads;
-                    if (xi > 8) continue;
-                    const uint32_t gp = (max_tiles * ngm) | 1u;
-                    const size_t meta = (size_t(tr) * 16 * gp * 4 * (a.meta == Meta::F32 ? 2 : 1) + 15) & ~size_t(15);
-                    const size_t img = size_t(max_tiles) * timg;
-                    // The MLP form: the finishers' sums of squares after the
-                    // reduction area, and a grid of both matrices.
-                    const size_t lds = meta + img + size_t(tr * kw) * a.batch * 16 * 4 +
-                                       (mlp ? size_t(tr * kw) * a.batch * 4 : 0);
-                    if (lds > lim.max_lds_per_block) continue;
-                    const double wgs = double(nbands) * ns * (mlp ? 2 : 1);
-                    const uint32_t resident = resident_per_cu(instance(a, xi, ring), threads, lds);
-                    if (wgs > double(resident) * cus) continue;
-                    const double waves = wgs * tr * kw;
-                    const double per_cu = std::ceil(wgs / cus) / (wgs / cus);
-                    double score = 0.5 * std::fabs(std::log2(waves / (2.0 * 4 * cus)));
-                    score += std::log2(per_cu);
-                    score += double(nbands) * a.batch * a.cols * 4.0 / wbytes;  // per matrix
-                    score += std::fabs(std::log2(waves / cus * ring * 2048.0 / 36864.0));
-                    score += ring == 2 ? 0.1 : 0.0;
-                    if (score < best - 1e-9) {
-                        best = score;
-                        pl.kw = kw;
-                        pl.tr = tr;
-                        pl.ns = ns;
-                        pl.nbands = nbands;
-                        pl.n_entries = n_entries;
-                        pl.tiles = tiles;
-                        pl.gp = gp;
-                        pl.meta_bytes = uint32_t(meta);
-                        pl.img_bytes = uint32_t(img);
-                        pl.xi = xi;
-                        pl.ring = ring;
-                        pl.lds = lds;
+    for (int pass = 0; pass < 2 && pl.kw == 0; ++pass) {
+        if (pass == 1 && (mlp || (force_ns && force_ns != 1))) break;
+        for (uint32_t ring : {2u, 3u}) {
+            if (force_ring && ring != force_ring) continue;
+            for (uint32_t ns = 1; ns <= 4; ++ns) {
+                if (force_ns && ns != force_ns) continue;
+                if (pass == 1 && ns != 1) continue;
+                if (ns > n_entries) continue;
+                uint32_t max_se = 0;
+                bool empty = false;
+                for (uint32_t sp = 0; sp < ns; ++sp) {
+                    const uint32_t e0 = host_split_begin(sp, ns, n_entries);
+                    const uint32_t e1 = host_split_begin(sp + 1, ns, n_entries);
+                    if (e1 <= e0) empty = true;
+                    else max_se = std::max(max_se, e1 - e0);
+                }
+                if (empty) continue;
+                const uint32_t max_tiles = std::min(max_se * tpe, tiles);
+                for (uint32_t tr : {1u, 2u, 4u, 8u}) {
+                    if (force_tr && tr != force_tr) continue;
+                    if (tr > 1 && (tr / 2) * 16 >= a.rows) continue;
+                    const uint32_t nbands = (row_tiles + tr - 1) / tr;
+                    for (uint32_t kw : {1u, 2u, 4u, 8u}) {
+                        if (force_kw && kw != force_kw) continue;
+                        const uint32_t threads = tr * kw * 64;
+                        if (threads > uint32_t(kMaxThreads) || kw > max_se) continue;
+                        if ((1u << meta_unit_shift(a, ns, n_entries)) > threads) continue;
+                        const uint32_t items = max_tiles * a.batch * 16;
+                        const uint32_t xi = (items + threads - 1) / threads;
+                        if (xi > 8) continue;
+                        const uint32_t gp = (max_tiles * ngm) | 1u;
+                        const size_t meta = (size_t(tr) * 16 * gp * 4 * (a.meta == Meta::F32 ? 2 : 1) + 15) & ~size_t(15);
+                        const size_t img = size_t(max_tiles) * timg;
+                        // The MLP form: the finishers' sums of squares after the
+                        // reduction area, and a grid of both matrices.
+                        const size_t lds = meta + img + size_t(tr * kw) * a.batch * 16 * 4 +
+                                           (mlp ? size_t(tr * kw) * a.batch * 4 : 0);
+                        if (lds > lim.max_lds_per_block) continue;
+                        const double wgs = double(nbands) * ns * (mlp ? 2 : 1);
+                        const uint32_t resident = resident_per_cu(instance(a, xi, ring), threads, lds);
+                        double score;
+                        if (pass == 0) {
+                            if (wgs > double(resident) * cus) continue;
+                            const double waves = wgs * tr * kw;
+                            const double per_cu = std::ceil(wgs / cus) / (wgs / cus);
+                            score = 0.5 * std::fabs(std::log2(waves / (2.0 * 4 * cus)));
+                            score += std::log2(per_cu);
+                            score += double(nbands) * a.batch * a.cols * 4.0 / wbytes;  // per matrix
+                            score += std::fabs(std::log2(waves / cus * ring * 2048.0 / 36864.0));
+                            score += ring == 2 ? 0.1 : 0.0;
+                        } else {
+                            const double flight = double(resident) * tr * kw * ring * 2048.0;
+                            score = double(8 / tr) + double(kw) + std::fabs(std::log2(flight / 49152.0));
+                        }
+                        if (score < best - 1e-9) {
+                            best = score;
+                            pl.kw = kw;
+                            pl.tr = tr;
+                            pl.ns = ns;
+                            pl.nbands = nbands;
+                            pl.n_entries = n_entries;
+                            pl.tiles = tiles;
+                            pl.gp = gp;
+                            pl.meta_bytes = uint32_t(meta);
+                            pl.img_bytes = uint32_t(img);
+                            pl.xi = xi;
+                            pl.ring = ring;
+                            pl.lds = lds;
+                        }
                     }
                 }
             }

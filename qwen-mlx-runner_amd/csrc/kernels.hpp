@@ -133,7 +133,7 @@ struct TilePlan {
     uint32_t meta_bytes = 0;  // LDS bytes of the staged metadata
     uint32_t img_bytes = 0;   // LDS bytes of the staged x images
     uint32_t xi = 0;          // x items staged per thread
-    uint32_t ring = 0;        // code entries in flight per wave (2, 3 or 4)
+    uint32_t ring = 0;        // code entries in flight per wave (2 or 3)
     size_t lds = 0;           // dynamic LDS bytes per workgroup
 };
 bool affine_tile_supported(const AffineArgs &a);

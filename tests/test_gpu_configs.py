@@ -85,6 +85,22 @@ def test_config3_vocabulary_head(gpu):
     check_dequant_rows(gpu, m, [0, rows - 1])
 
 
+def test_multi_round_band_plan_on_a_ragged_tall_matrix(gpu):
+    """A matrix too tall for any one-round row-band plan, with a partial
+    last tile and band: single-split bands over several rounds of
+    workgroups, against the oracle on sampled rows (the tail rows
+    included), deterministic across launches."""
+    rows, cols, batch = 140001, 4096, 2
+    m = synth.q4_bf16_matrix(rows, cols, SEED, tag="tall")
+    sample = sorted(set(list(range(0, rows, 89)) + [rows - 16, rows - 2, rows - 1]))
+    gpu.set_gemv_plan(0, 0)
+    first = check(gpu, m, batch, sample)
+    kernel = gpu.last_hip_kernel()
+    assert kernel.startswith("affine_band_kernel ring=") and kernel.endswith(" ns=1 tr=8 kw=1"), kernel
+    again = check(gpu, m, batch, sample)
+    assert np.array_equal(first.view(np.uint32), again.view(np.uint32)), "launches differ"
+
+
 @pytest.mark.parametrize("batch", [128, 256])
 def test_config4_wide_block(gpu, batch):
     rows, cols = synth.MLP_SHAPES["gate_up"]

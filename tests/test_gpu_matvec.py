@@ -233,15 +233,19 @@ def test_row_kernel_is_deterministic(gpu, rows, cols, batch):
 
 @pytest.mark.parametrize("rows,cols,bits,batch,kind", [
     (5120, 17408, 4, 1, -4), (17408, 5120, 4, 3, -4), (5120, 5120, 4, 1, -4), (5120, 17408, 8, 1, -4),
-    (5120, 5120, 8, 3, -4), (151936, 5120, 4, 1, -3), (151936, 5120, 4, 3, -3)])
+    (5120, 5120, 8, 3, -4), (151936, 5120, 4, 1, -4), (151936, 5120, 4, 3, -4)])
 def test_default_plan_kernel_family(gpu, rows, cols, bits, batch, kind):
-    """The default planner takes the row-band kernel wherever it has a plan
-    whose workgroups are all resident in one round (the Q4 and Q8 MLP
-    shapes, 5120x5120 projections), and the row-owning kernel where no such
-    plan exists (the vocabulary head)."""
+    """The default planner takes the row-band kernel: a plan whose
+    workgroups are all resident in one round where one exists (the Q4 and
+    Q8 MLP shapes, 5120x5120 projections), else single-split bands over
+    several rounds (the vocabulary head: 8 tiles per band, one wave per
+    tile; the two-entry ring at B=1, with two workgroups per CU, and the
+    three-entry ring at B=3, with one)."""
     gpu.set_gemv_plan(0, 0)
     plan = gpu.gemv_plan(rows, cols, bits, batch)
     assert plan[0] == kind, f"{rows}x{cols} B{batch}: expected plan kind {kind}, got {plan}"
+    if rows == 151936:
+        assert plan[1] == (210801 if batch == 1 else 310801), plan
 
 
 @pytest.mark.parametrize("rr,name,batch", [(0, "matmul_affine_bf16", 1), (0, "matmul_affine_bf16", 3),
