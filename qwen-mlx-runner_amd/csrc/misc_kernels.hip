@@ -110,22 +110,27 @@ __global__ __launch_bounds__(256) void dense_f16_kernel(const uint16_t *__restri
 }
 
 // Dense F16 weights times token-major FP32 x, streaming form for cols % 8 == 0
-// and matrices under 2 GB: one wave per R rows, each lane taking 8
-// consecutive columns per 512-column step as one 16-byte weight load per row
-// (buffer loads; rows past the matrix read as zeros). The x slice of a step
-// is loaded once and used for the R rows, and every RHS uses the same
-// weight registers, so the matrix is read once whatever B. Two steps are
-// requested before the first is used.
-template <int B, int R>
+// and matrices under 2 GB: each lane takes 8 consecutive columns per
+// 512-column step as one 16-byte weight load per row (buffer loads; rows past
+// the matrix read as zeros). The x slice of a step is loaded once and used
+// for the wave's R rows, and every RHS uses the same weight registers, so the
+// matrix is read once whatever B. Two steps are requested before the first
+// is used. KS = 1: each of the workgroup's four waves owns R rows for all of
+// K. KS = 4: the four waves share R rows, wave k taking steps k, k + 4, ...;
+// their sums meet in LDS and are added in wave order, so results do not
+// depend on timing.
+template <int B, int R, int KS>
 __global__ __launch_bounds__(256) void dense_f16_stream_kernel(const uint16_t *__restrict__ w,
                                                                const float *__restrict__ x,
                                                                float *__restrict__ y, uint32_t rows,
                                                                uint32_t cols, uint32_t w_bytes) {
+    static_assert(KS == 1 || KS == 4, "one wave per row group, or the workgroup's four");
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));
     typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * R;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t row0 = KS == 1 ? (blockIdx.x * 4u + wave) * R : blockIdx.x * R;
     const uint32_t lane = threadIdx.x & 63;
-    if (row0 >= rows) return;  // the whole wave
+    if (KS == 1 && row0 >= rows) return;  // the whole wave (KS = 4: the grid covers rows exactly)
     const __amdgpu_buffer_rsrc_t wr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(w), 0, int(w_bytes), mfma::kRsrcWord3);
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
@@ -169,22 +174,43 @@ __global__ __launch_bounds__(256) void dense_f16_stream_kernel(const uint16_t *_
         }
     };
     const uint32_t steps = (cols + 511) / 512;
+    const uint32_t first = KS == 1 ? 0u : wave;
+    constexpr uint32_t STRIDE = 512u * KS;  // columns between a wave's steps
     v4u w0[R], w1[R];
-    load_w(w0, lane * 8u);
-    for (uint32_t st = 0; st < steps; st += 2) {
+    load_w(w0, first * 512u + lane * 8u);
+    for (uint32_t st = first; st < steps; st += 2 * KS) {
         const uint32_t c0 = st * 512u + lane * 8u;
-        load_w(w1, c0 + 512u);
+        load_w(w1, c0 + STRIDE);
         use(w0, c0);
-        load_w(w0, c0 + 1024u);
-        use(w1, c0 + 512u);
+        load_w(w0, c0 + 2 * STRIDE);
+        use(w1, c0 + STRIDE);
     }
+    if constexpr (KS == 1) {
 #pragma unroll
-    for (int i = 0; i < R; ++i)
+        for (int i = 0; i < R; ++i)
 #pragma unroll
-        for (int t = 0; t < B; ++t) {
-            const float v = wave_sum(acc[i][t]);
-            if (lane == 0 && row0 + i < rows) y[size_t(t) * rows + row0 + i] = v;
+            for (int t = 0; t < B; ++t) {
+                const float v = wave_sum(acc[i][t]);
+                if (lane == 0 && row0 + i < rows) y[size_t(t) * rows + row0 + i] = v;
+            }
+    } else {
+        __shared__ float part[KS][R][B];
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int t = 0; t < B; ++t) {
+                const float v = wave_sum(acc[i][t]);
+                if (lane == 0) part[wave][i][t] = v;
+            }
+        __syncthreads();
+        if (threadIdx.x < uint32_t(R * B)) {
+            const uint32_t i = threadIdx.x / B, t = threadIdx.x % B;
+            float v = part[0][i][t];
+#pragma unroll
+            for (int k = 1; k < KS; ++k) v += part[k][i][t];
+            if (row0 + i < rows) y[size_t(t) * rows + row0 + i] = v;
         }
+    }
 }
 
 __global__ __launch_bounds__(256) void embed_f16_kernel(const uint16_t *__restrict__ w,
@@ -213,18 +239,57 @@ hipError_t launch_embed_affine(const uint32_t *w, const void *s, const void *b, 
     return hipGetLastError();
 }
 
+namespace {
+
+// Rows per wave and waves per row group of the streaming dense kernel.
+struct DenseShape {
+    uint32_t r, ks;
+};
+
+// Eight rows per wave at four RHS (half the x loads per weight), else four.
+// The four waves of a workgroup split K (four times the waves), except at
+// three or more RHS where one wave per row group already gives four waves
+// per SIMD on 256 CUs. Measured on MI355X (us, interleaved, one box), one
+// wave per row group and four rows -> this rule:
+//   5120x17408  B=1 36.6 -> 32.0, B=2 44.0 -> 38.0, B=3 50.4 -> 45.7, B=4 62.0 -> 44.4
+//   17408x5120  B=1 33.1 -> 30.5, B=2 38.5 -> 38.2, B=3 43.7 (kept), B=4 47.3 -> 46.2
+// Each case is the best of (4 or 8 rows) x (one or four waves per group).
+DenseShape dense_shape(uint32_t rows, uint32_t batch) {
+    const uint32_t r = batch == 4 ? 8u : 4u;
+    const bool filled = rows / r >= 4u * 4u * 256u;
+    return DenseShape{r, filled && batch >= 3 ? 1u : 4u};
+}
+
+template <int B, int R, int KS>
+void launch_dense_stream(const uint16_t *w, const float *x, float *y, uint32_t rows, uint32_t cols,
+                         uint32_t w_bytes, hipStream_t stream) {
+    const uint32_t blocks = KS == 1 ? (rows + 4 * R - 1) / (4 * R) : (rows + R - 1) / R;
+    hipLaunchKernelGGL((dense_f16_stream_kernel<B, R, KS>), dim3(blocks), dim3(256), 0, stream, w, x, y, rows,
+                       cols, w_bytes);
+}
+
+template <int B>
+void launch_dense_batch(DenseShape sh, const uint16_t *w, const float *x, float *y, uint32_t rows, uint32_t cols,
+                        uint32_t w_bytes, hipStream_t stream) {
+    if (sh.ks == 1) launch_dense_stream<B, 4, 1>(w, x, y, rows, cols, w_bytes, stream);
+    else if (sh.r == 8) launch_dense_stream<B, 8, 4>(w, x, y, rows, cols, w_bytes, stream);
+    else launch_dense_stream<B, 4, 4>(w, x, y, rows, cols, w_bytes, stream);
+}
+
+}  // namespace
+
 hipError_t launch_dense_f16(const uint16_t *w, const float *x, float *y, uint32_t rows,
                             uint32_t cols, uint32_t batch, hipStream_t stream) {
-    constexpr uint32_t R = 4;
     const uint64_t w_bytes = uint64_t(rows) * cols * 2;
     if (cols % 8 == 0 && w_bytes < (1ull << 31) && uint64_t(batch) * cols * 4 < (1ull << 31) && batch >= 1 &&
         batch <= 4) {
-        const uint32_t blocks = (rows + 4 * R - 1) / (4 * R);
+        const DenseShape sh = dense_shape(rows, batch);
+        const uint32_t wb = uint32_t(w_bytes);
         switch (batch) {
-            case 1: hipLaunchKernelGGL((dense_f16_stream_kernel<1, R>), dim3(blocks), dim3(256), 0, stream, w, x, y, rows, cols, uint32_t(w_bytes)); break;
-            case 2: hipLaunchKernelGGL((dense_f16_stream_kernel<2, R>), dim3(blocks), dim3(256), 0, stream, w, x, y, rows, cols, uint32_t(w_bytes)); break;
-            case 3: hipLaunchKernelGGL((dense_f16_stream_kernel<3, R>), dim3(blocks), dim3(256), 0, stream, w, x, y, rows, cols, uint32_t(w_bytes)); break;
-            default: hipLaunchKernelGGL((dense_f16_stream_kernel<4, R>), dim3(blocks), dim3(256), 0, stream, w, x, y, rows, cols, uint32_t(w_bytes)); break;
+            case 1: launch_dense_batch<1>(sh, w, x, y, rows, cols, wb, stream); break;
+            case 2: launch_dense_batch<2>(sh, w, x, y, rows, cols, wb, stream); break;
+            case 3: launch_dense_batch<3>(sh, w, x, y, rows, cols, wb, stream); break;
+            default: launch_dense_batch<4>(sh, w, x, y, rows, cols, wb, stream); break;
         }
         return hipGetLastError();
     }

@@ -284,11 +284,14 @@ def test_matrix_core_kernels_read_x_at_4_byte_offsets(gpu, rr, name, batch):
 
 
 @pytest.mark.parametrize("rows,cols,batch", [
-    (5120, 17408, 1), (17408, 5120, 3), (301, 4104, 2), (1000, 8, 4), (77, 1001, 1), (33, 512, 4)])
+    (5120, 17408, 1), (17408, 5120, 3), (5120, 17408, 4), (301, 4104, 2), (4099, 2056, 3), (1000, 8, 4),
+    (77, 1001, 1), (33, 512, 4)])
 def test_dense_f16_products_at_scale(gpu, rows, cols, batch):
     """matvec_f16 / matmul_f16 (kernels/qwen.metal:48-57,
     kernels/matmul_block.metal:213-248) against the FP64 oracle: the
-    streaming kernel (cols % 8 == 0, any row tail, 1-4 RHS) and the simple
+    streaming kernel (cols % 8 == 0, any row tail, 1-4 RHS) in its three
+    shapes (four waves splitting K over 4 or 8 rows, one wave per 4 rows at
+    17408x5120 B=3; partial last steps and row groups), and the simple
     kernel (cols % 8 != 0)."""
     rng = np.random.default_rng(rows * 3 + cols + batch)
     w16 = rng.standard_normal(rows * cols).astype(np.float16).view(np.uint16)
