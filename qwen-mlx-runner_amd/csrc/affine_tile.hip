@@ -60,7 +60,6 @@ namespace qmr {
 namespace band {
 
 constexpr int kMaxThreads = 512;  // up to 8 waves: x staging needs up to 8 items of registers per thread
-constexpr int kMetaUnits = 4;  // 16-byte metadata loads per thread and plane (fast path)
 
 struct BandParams {
     const uint32_t *w;
@@ -76,7 +75,7 @@ struct BandParams {
     const void *b2;
     const float *norm;
     float eps;
-    unsigned long long *partial;  // {value, epoch} slots: [ns-1][B][rows], or [2*ns][B][rows] for the MLP form
+    unsigned long long *partial;  // {value, epoch} slots: [ns-1][B][rows], or [ns-1][gate, up][B][rows] (MLP form)
     uint32_t epoch;
     uint32_t spin_limit;
     uint32_t rows, cols;
@@ -111,22 +110,16 @@ namespace {
 using namespace mfma;
 using band::BandParams;
 using band::kMaxThreads;
-using band::kMetaUnits;
 
-template <int BITS, int GROUP, int B>
-constexpr uint32_t tile_img_bytes() {
-    constexpr int NGM = kTileK / GROUP;
-    constexpr int HALF = 16 / NGM / 2;
-    return 4u * 4 * 2 * B * 16 + uint32_t(NGM) * (HALF / 2) * 16;
-}
+constexpr int kMetaUnits = 4;  // 16-byte metadata loads per thread and plane (fast path)
 
 // XI: x items (8 columns each) staged per thread. FUSE 0: y = W x; 1: y =
 // r + W x; 2: the fused MLP form, y = silu(G x^) * (U x^) with x^ =
-// rms_norm(x) * norm: the grid holds the gate's bands and splits, then the
-// up matrix's; x is staged times the norm weights, every workgroup but the
-// up matrix's last split of a band publishes its sums, and that one adds
-// the gate's and up's sums in split order and applies 1/rms (the products
-// are linear in it) and SwiGLU.
+// rms_norm(x) * norm: a band's first TR/2 tiles are gate rows and its last
+// TR/2 the up rows with the same indices, so x (staged times the norm
+// weights) serves both; the band's last split adds each row's gate and up
+// sums in split order and applies 1/rms (the products are linear in it) and
+// SwiGLU.
 template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE>
 __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) {
     constexpr bool MLP = FUSE == 2;
@@ -137,7 +130,6 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     constexpr int TPE = 8 / BITS;        // K tiles per 128-byte entry
     constexpr int MB = META == 0 ? 4 : 2;
     constexpr int VEC = 16 / MB;  // metadata values per 16-byte load
-    constexpr uint32_t TIMG = tile_img_bytes<BITS, GROUP, B>();
     constexpr uint32_t TIMG_A = 4u * 4 * 2 * B * 16;
     static_assert(2 * B <= SLOTS, "batch does not fit the slot layout");
 
@@ -151,15 +143,15 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const uint32_t KW = p.kw;
     const uint32_t ti = uint32_t(wave) >> p.kw_shift;
     const uint32_t kw = uint32_t(wave) & (KW - 1u);
-    const uint32_t per_mat = p.nbands * p.ns;
-    const uint32_t mat = MLP ? blockIdx.x / per_mat : 0u;  // 0: w/s/b (the gate), 1: the up matrix
-    const uint32_t bid = blockIdx.x - mat * per_mat;
-    const uint32_t band = bid % p.nbands;
-    const uint32_t split = bid / p.nbands;
-    // The MLP form's finishing workgroups: the up matrix's last split.
-    const bool finisher = MLP && mat == 1 && split + 1 == p.ns;
-    const uint32_t band_row0 = band * p.tr * 16u;
-    const uint32_t tile_row0 = band_row0 + ti * 16u;
+    const uint32_t band = blockIdx.x % p.nbands;
+    const uint32_t split = blockIdx.x / p.nbands;
+    // The MLP form: tiles [0, H) of a band are gate rows, [H, 2H) the up
+    // matrix's rows with the same indices; the band's last split finishes.
+    const uint32_t H = MLP ? p.tr / 2u : p.tr;  // row tiles per matrix in a band
+    const bool up_tile = MLP && ti >= H;        // wave-uniform
+    const bool finisher = MLP && split + 1 == p.ns;
+    const uint32_t band_row0 = band * H * 16u;
+    const uint32_t tile_row0 = band_row0 + (up_tile ? ti - H : ti) * 16u;
     const uint32_t nG = p.cols / GROUP;
     const uint32_t Gp = p.gp;
     // The split's entries (from the host: a uniform select, no division),
@@ -187,15 +179,21 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     float *red = reinterpret_cast<float *>(lds + p.meta_bytes + p.img_bytes);
     float *sq = red + p.tr * KW * B * 16u;  // MLP: [wave][B] partial sums of x^2 (finishers)
 
-    const uint32_t *wp = MLP && mat ? p.w2 : p.w;
-    const void *sp_ = MLP && mat ? p.s2 : p.s;
-    const void *bp = MLP && mat ? p.b2 : p.b;
-    const __amdgpu_buffer_rsrc_t wr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(wp), 0, int(p.w_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t *>(up_tile ? p.w2 : p.w), 0, int(p.w_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t sr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(sp_), 0, int(p.m_bytes), kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.s), 0, int(p.m_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t br =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(bp), 0, int(p.m_bytes), kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.b), 0, int(p.m_bytes), kRsrcWord3);
+    // The MLP form's up-matrix metadata. A staged row's loads go to both
+    // matrices, the other matrix's through kOut (zeros), and are OR-ed: the
+    // row's matrix differs between lanes, and a per-lane buffer resource
+    // would put every load in a readfirstlane loop.
+    const __amdgpu_buffer_rsrc_t sr2 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(MLP ? p.s2 : p.s), 0, int(p.m_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t br2 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(MLP ? p.b2 : p.b), 0, int(p.m_bytes), kRsrcWord3);
+    const uint32_t mat_rows = H * 16u;  // staged rows per matrix
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(p.x), 0, int(uint32_t(B) * p.cols * 4u), kRsrcWord3);
 
@@ -257,14 +255,29 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const uint32_t urow = uint32_t(tid) >> p.unit_shift;
     const uint32_t rstep = uint32_t(nthr) >> p.unit_shift;
     const bool ucol_ok = ucol < upr;
-    auto unit_off = [&](uint32_t rl) -> uint32_t { return ((band_row0 + rl) * nG + Ga) * MB + ucol * 16u; };
+    // Staged row rl is matrix row band_row0 + rl (the MLP form: rows past
+    // mat_rows are the up matrix's rows rl - mat_rows).
+    auto mrow = [&](uint32_t rl) -> uint32_t { return band_row0 + (MLP && rl >= mat_rows ? rl - mat_rows : rl); };
+    auto unit_off = [&](uint32_t rl) -> uint32_t { return (mrow(rl) * nG + Ga) * MB + ucol * 16u; };
+    auto load_units = [&](uint32_t rl, uint32_t off, u4 &sv, u4 &bv) {
+        if constexpr (MLP) {
+            const bool up_row = rl >= mat_rows;
+            const uint32_t og = up_row ? kOut : off, ou = up_row ? off : kOut;
+            sv = __builtin_amdgcn_raw_buffer_load_b128(sr, int(og), 0, 0) |
+                 __builtin_amdgcn_raw_buffer_load_b128(sr2, int(ou), 0, 0);
+            bv = __builtin_amdgcn_raw_buffer_load_b128(br, int(og), 0, 0) |
+                 __builtin_amdgcn_raw_buffer_load_b128(br2, int(ou), 0, 0);
+        } else {
+            sv = __builtin_amdgcn_raw_buffer_load_b128(sr, int(off), 0, 0);
+            bv = __builtin_amdgcn_raw_buffer_load_b128(br, int(off), 0, 0);
+        }
+    };
     u4 ms[kMetaUnits], mbv[kMetaUnits];
 #pragma unroll
     for (int u = 0; u < kMetaUnits; ++u) {
         const uint32_t rl = urow + uint32_t(u) * rstep;
         const uint32_t off = (ucol_ok && rl < band_rows) ? unit_off(rl) : kOut;
-        ms[u] = __builtin_amdgcn_raw_buffer_load_b128(sr, int(off), 0, 0);
-        mbv[u] = __builtin_amdgcn_raw_buffer_load_b128(br, int(off), 0, 0);
+        load_units(rl, off, ms[u], mbv[u]);
     }
 
     // ---- 3. The first P entries of codes. An entry is 128 contiguous bytes
@@ -356,9 +369,9 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
             }
             // Bands with more rows than the unrolled loads cover read the rest here.
             for (uint32_t rl = urow + uint32_t(kMetaUnits) * rstep; rl < band_rows; rl += rstep) {
-                const uint32_t off = unit_off(rl);
-                put(rl, __builtin_amdgcn_raw_buffer_load_b128(sr, int(off), 0, 0),
-                    __builtin_amdgcn_raw_buffer_load_b128(br, int(off), 0, 0));
+                u4 sv, bv;
+                load_units(rl, unit_off(rl), sv, bv);
+                put(rl, sv, bv);
             }
         }
     } else {
@@ -366,13 +379,25 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         for (uint32_t f = uint32_t(tid); f < p.tr * 16u * ng; f += uint32_t(nthr)) {
             const uint32_t rl = f / ng;
             const uint32_t g = f - rl * ng;
-            const uint32_t off = ((band_row0 + rl) * nG + G0 + g) * MB;
+            const uint32_t off = (mrow(rl) * nG + G0 + g) * MB;
+            const bool up_row = MLP && rl >= mat_rows;
+            const uint32_t og = up_row ? kOut : off, ou = up_row ? off : kOut;
             if constexpr (META == 0) {
-                ldsM[(rl * Gp + g) * 2] = __builtin_amdgcn_raw_buffer_load_b32(sr, int(off), 0, 0);
-                ldsM[(rl * Gp + g) * 2 + 1] = __builtin_amdgcn_raw_buffer_load_b32(br, int(off), 0, 0);
+                uint32_t sv = __builtin_amdgcn_raw_buffer_load_b32(sr, int(og), 0, 0);
+                uint32_t bv = __builtin_amdgcn_raw_buffer_load_b32(br, int(og), 0, 0);
+                if constexpr (MLP) {
+                    sv |= __builtin_amdgcn_raw_buffer_load_b32(sr2, int(ou), 0, 0);
+                    bv |= __builtin_amdgcn_raw_buffer_load_b32(br2, int(ou), 0, 0);
+                }
+                ldsM[(rl * Gp + g) * 2] = sv;
+                ldsM[(rl * Gp + g) * 2 + 1] = bv;
             } else {
-                const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(sr, int(off), 0, 0);
-                const uint32_t bv = __builtin_amdgcn_raw_buffer_load_b16(br, int(off), 0, 0);
+                uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(sr, int(og), 0, 0);
+                uint32_t bv = __builtin_amdgcn_raw_buffer_load_b16(br, int(og), 0, 0);
+                if constexpr (MLP) {
+                    sv |= __builtin_amdgcn_raw_buffer_load_b16(sr2, int(ou), 0, 0);
+                    bv |= __builtin_amdgcn_raw_buffer_load_b16(br2, int(ou), 0, 0);
+                }
                 ldsM[rl * Gp + g] = (sv & 0xFFFFu) | (bv << 16);
             }
         }
@@ -458,16 +483,22 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         if (t0 + 1 < B) dst[size_t(t0 + 1) * 16u] = v1;
     }
     __syncthreads();
-    const uint32_t outs = p.tr * 16u * B;
+    // One thread per output row and RHS (the MLP form: per gate row, whose
+    // up row is H tiles further down the band).
+    const uint32_t outs = H * 16u * B;
     if (uint32_t(tid) >= outs) return;
-    const uint32_t tt = uint32_t(tid) / (16u * B);  // tile within the band
+    const uint32_t tt = uint32_t(tid) / (16u * B);  // tile within the band (of the gate rows)
     const uint32_t t = (uint32_t(tid) / 16u) % B;
     const uint32_t rr = uint32_t(tid) % 16u;
     const uint32_t row = band_row0 + tt * 16u + rr;
     if (row >= p.rows) return;
-    const float *src = red + (size_t(tt * KW) * B + t) * 16u + rr;
-    float v = src[0];
-    for (uint32_t k = 1; k < KW; ++k) v += src[size_t(k) * B * 16u];
+    auto wave_sum_of = [&](uint32_t tile) -> float {
+        const float *src = red + (size_t(tile * KW) * B + t) * 16u + rr;
+        float sum = src[0];
+        for (uint32_t k = 1; k < KW; ++k) sum += src[size_t(k) * B * 16u];
+        return sum;
+    };
+    float v = wave_sum_of(tt);
     const size_t oy = size_t(t) * p.rows + row;
     const size_t stride = size_t(B) * p.rows;
     // Reads slot set k's value for oy once its epoch is this launch's;
@@ -485,25 +516,29 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         }
         return __uint_as_float(uint32_t(word));
     };
-    auto publish = [&](uint32_t k) {
-        const unsigned long long word = (static_cast<unsigned long long>(p.epoch) << 32) | __float_as_uint(v);
+    auto publish = [&](uint32_t k, float value) {
+        const unsigned long long word = (static_cast<unsigned long long>(p.epoch) << 32) | __float_as_uint(value);
         __hip_atomic_store(p.partial + size_t(k) * stride + oy, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     if constexpr (MLP) {
-        // Slot sets [mat*ns + split]. The finisher adds the gate's splits and
-        // then the up matrix's, in split order.
+        // Slot sets [2*split] (gate) and [2*split + 1] (up) for splits
+        // 0..ns-2; the band's last split adds each in split order.
+        const float vu = wave_sum_of(tt + H);
         if (!finisher) {
-            publish(mat * p.ns + split);
+            publish(2 * split, v);
+            publish(2 * split + 1, vu);
             return;
         }
         bool ok = true;
-        float g = take(0, ok);
-        for (uint32_t k = 1; k < p.ns; ++k) g += take(k, ok);
-        float u = v;
+        float g = v, u = vu;
         if (p.ns > 1) {
-            float su = take(p.ns, ok);
-            for (uint32_t k = 1; k + 1 < p.ns; ++k) su += take(p.ns + k, ok);
-            u = su + v;
+            float sg = take(0, ok), su = take(1, ok);
+            for (uint32_t k = 1; k + 1 < p.ns; ++k) {
+                sg += take(2 * k, ok);
+                su += take(2 * k + 1, ok);
+            }
+            g = sg + v;
+            u = su + vu;
         }
         float ss = 0.f;
         for (uint32_t wv = 0; wv < p.tr * KW; ++wv) ss += sq[wv * B + t];
@@ -514,7 +549,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     } else {
         if (p.ns > 1) {
             if (split + 1 < p.ns) {
-                publish(split);
+                publish(split, v);
                 return;
             }
             // The band's last split: the other splits' sums, in split order.
@@ -537,8 +572,7 @@ hipError_t launch_inst(const BandParams &p, const TilePlan &pl, hipStream_t stre
         if (e != hipSuccess) return e;
         configured = pl.lds;
     }
-    const uint32_t mats = FUSE == 2 ? 2u : 1u;
-    hipLaunchKernelGGL(kernel, dim3(mats * pl.nbands * pl.ns), dim3(pl.tr * pl.kw * 64), pl.lds, stream, p);
+    hipLaunchKernelGGL(kernel, dim3(pl.nbands * pl.ns), dim3(pl.tr * pl.kw * 64), pl.lds, stream, p);
     return hipGetLastError();
 }
 
@@ -804,8 +838,11 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                 const uint32_t max_tiles = std::min(max_se * tpe, tiles);
                 for (uint32_t tr : {1u, 2u, 4u, 8u}) {
                     if (force_tr && tr != force_tr) continue;
-                    if (tr > 1 && (tr / 2) * 16 >= a.rows) continue;
-                    const uint32_t nbands = (row_tiles + tr - 1) / tr;
+                    // The MLP form: tr/2 gate tiles and tr/2 up tiles per band.
+                    if (mlp && tr < 2) continue;
+                    const uint32_t h = mlp ? tr / 2 : tr;  // row tiles per matrix in a band
+                    if (h > 1 && (h / 2) * 16 >= a.rows) continue;
+                    const uint32_t nbands = (row_tiles + h - 1) / h;
                     for (uint32_t kw : {1u, 2u, 4u, 8u}) {
                         if (force_kw && kw != force_kw) continue;
                         const uint32_t threads = tr * kw * 64;
@@ -818,11 +855,11 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                         const size_t meta = (size_t(tr) * 16 * gp * 4 * (a.meta == Meta::F32 ? 2 : 1) + 15) & ~size_t(15);
                         const size_t img = size_t(max_tiles) * timg;
                         // The MLP form: the finishers' sums of squares after the
-                        // reduction area, and a grid of both matrices.
+                        // reduction area.
                         const size_t lds = meta + img + size_t(tr * kw) * a.batch * 16 * 4 +
                                            (mlp ? size_t(tr * kw) * a.batch * 4 : 0);
                         if (lds > lim.max_lds_per_block) continue;
-                        const double wgs = double(nbands) * ns * (mlp ? 2 : 1);
+                        const double wgs = double(nbands) * ns;
                         const uint32_t resident = resident_per_cu(instance(a, xi, ring), threads, lds);
                         double score;
                         if (pass == 0) {
@@ -831,7 +868,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                             const double per_cu = std::ceil(wgs / cus) / (wgs / cus);
                             score = 0.5 * std::fabs(std::log2(waves / (2.0 * 4 * cus)));
                             score += std::log2(per_cu);
-                            score += double(nbands) * a.batch * a.cols * 4.0 / wbytes;  // per matrix
+                            score += double(nbands) * a.batch * a.cols * 4.0 / (wbytes * (mlp ? 2 : 1));
                             score += std::fabs(std::log2(waves / cus * ring * 2048.0 / 36864.0));
                             score += ring == 2 ? 0.1 : 0.0;
                         } else {
@@ -862,15 +899,14 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
 }
 
 size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a) {
-    if (a.up_w) return size_t(2) * pl.ns * a.batch * a.rows * sizeof(unsigned long long);
     if (pl.ns <= 1) return 0;
-    return size_t(pl.ns - 1) * a.batch * a.rows * sizeof(unsigned long long);
+    return size_t(pl.ns - 1) * (a.up_w ? 2 : 1) * a.batch * a.rows * sizeof(unsigned long long);
 }
 
 hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial, uint32_t epoch,
                               hipStream_t stream) {
     if (pl.kw == 0) return hipErrorInvalidValue;
-    if ((pl.ns > 1 || a.up_w) && partial == nullptr) return hipErrorInvalidValue;
+    if (pl.ns > 1 && partial == nullptr) return hipErrorInvalidValue;
     BandParams p;
     p.w = a.w;
     p.s = a.s;

@@ -956,9 +956,10 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
                 std::memcpy(&a.eps, &params[5], 4);
                 ensure(qmr::affine_rows_supported(a), name + ": no fused kernel for this format",
                        QMR_ERR_UNSUPPORTED);
-                // The row-band kernel's MLP form where it has a one-round
-                // plan for both matrices' grid (or the tuning hook forces it,
-                // rr == -4); else the split-K kernel (measured at 17408x5120:
+                // The row-band kernel's MLP form (bands of gate tiles and the
+                // up tiles of the same rows) where it has a one-round plan (or
+                // the tuning hook forces it, rr == -4); else the split-K
+                // kernel (measured at 17408x5120:
                 // 26.1 us at B=1 and 30.4 at B=3 against 29.4 and 35.5 for
                 // the row-owning MLP mode, although both matrices' grid takes
                 // two rounds of resident workgroups), also when the hook asks

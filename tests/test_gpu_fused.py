@@ -77,13 +77,42 @@ def test_mlp_gate_up_swiglu_matches_unfused_oracle(gpu, rr, rows, cols, bits, gr
         gpu.set_gemv_plan(0, 0)
 
 
+@pytest.mark.parametrize("plan", [310201, 220401, 330402, 240801, 210204])
+@pytest.mark.parametrize("rows,cols,bits,group,batch,kind", [
+    (2000, 3072, 4, 64, 2, "bf16"), (1000, 1024, 8, 64, 1, "f16"), (300, 2048, 4, 32, 2, "f32")])
+def test_mlp_band_form_forced_plans(gpu, plan, rows, cols, bits, group, batch, kind):
+    """The row-band kernel's MLP form under forced plans (rr -4, ks = ring *
+    100000 + splits * 10000 + tiles * 100 + waves): one to four K splits
+    (the gate and up slot planes), bands of one to four gate tiles with as
+    many up tiles, one to four waves per tile, row tails; against the FP64
+    oracle and deterministic."""
+    rng = np.random.default_rng(plan % 9973 + rows + batch)
+    gate_m = _matrix(rng, rows, cols, bits, group, kind)
+    up_m = _matrix(rng, rows, cols, bits, group, kind)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    want = oracle.mlp_gate_up_f64(gate_m, up_m, kind, x, nw, EPS, rows, cols, bits, group, batch, 8)
+    gpu.set_gemv_plan(-4, plan)
+    try:
+        got = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind)
+        kernel = gpu.last_hip_kernel()
+        again = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind)
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    ring, ns, tr, kw = plan // 100000, plan // 10000 % 10, plan // 100 % 100, plan % 100
+    assert kernel == f"affine_band_kernel ring={ring} ns={ns} tr={tr} kw={kw} (MLP)", kernel
+    assert_gate(got, want, f"mlp band {plan} {rows}x{cols} Q{bits}/g{group} {kind} B{batch}")
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "launches differ"
+
+
 @pytest.mark.parametrize("batch", [1, 3])
 def test_mlp_default_is_the_band_kernel_at_the_27b_shape(gpu, batch):
     """At the 27B gate/up shape and B=1 the fused form runs on the row-band
-    kernel (both matrices in one grid, the up matrix's last split
-    finishing). At B=3 both matrices' workgroups do not fit one round of
-    resident workgroups (their x images take 32-64 KB of LDS each), so the
-    split-K kernel runs it."""
+    kernel: each band holds gate tiles and the up tiles of the same rows, so
+    one staging of x serves both matrices and the grid is one matrix's. At
+    B=3 the form's instances hold x and the norm weights together while
+    staging (175-183 VGPRs: one 512-thread workgroup per CU), no plan fits
+    one round of resident workgroups, and the split-K kernel runs it."""
     rows, cols = 17408, 5120
     rng = np.random.default_rng(batch)
     gate_m = _matrix(rng, rows, cols, 4, 64, "bf16")
