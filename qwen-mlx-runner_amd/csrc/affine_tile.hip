@@ -592,13 +592,15 @@ hipError_t launch_xi(const BandParams &p, const TilePlan &pl, hipStream_t stream
 // x items per thread: the smallest compiled count that covers the plan's.
 // Every unrolled item issues its loads (dead ones read zeros), so the
 // metric shapes get exact counts: 2 at B=1 and 5 at B=3 (5120x17408, three
-// splits), each 0.15-0.2 us faster than rounding up to 4 and 8.
-constexpr uint32_t xi_instance(uint32_t xi) { return xi <= 2 ? 2 : xi <= 4 ? 4 : xi <= 5 ? 5 : 8; }
+// splits), each 0.15-0.2 us faster than rounding up to 4 and 8; 3 serves
+// 17408x5120 at B=1 (two splits), plain and MLP form.
+constexpr uint32_t xi_instance(uint32_t xi) { return xi <= 2 ? 2 : xi <= 3 ? 3 : xi <= 4 ? 4 : xi <= 5 ? 5 : 8; }
 
 template <int BITS, int META, int GROUP, int B>
 hipError_t launch_b(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
     switch (xi_instance(pl.xi)) {
         case 2: return launch_xi<BITS, META, GROUP, B, 2>(p, pl, stream);
+        case 3: return launch_xi<BITS, META, GROUP, B, 3>(p, pl, stream);
         case 4: return launch_xi<BITS, META, GROUP, B, 4>(p, pl, stream);
         case 5: return launch_xi<BITS, META, GROUP, B, 5>(p, pl, stream);
         default: return launch_xi<BITS, META, GROUP, B, 8>(p, pl, stream);
@@ -637,6 +639,7 @@ const void *instance_group(uint32_t batch, uint32_t xi, uint32_t ring, bool mlp)
         };
         switch (xi_instance(xi)) {
             case 2: return by_ring(std::integral_constant<int, 2>{});
+            case 3: return by_ring(std::integral_constant<int, 3>{});
             case 4: return by_ring(std::integral_constant<int, 4>{});
             case 5: return by_ring(std::integral_constant<int, 5>{});
             default: return by_ring(std::integral_constant<int, 8>{});
