@@ -75,7 +75,7 @@ struct BandParams {
     const void *b2;
     const float *norm;
     float eps;
-    unsigned long long *partial;  // {value, epoch} slots: [ns-1][B][rows], or [ns-1][gate, up][B][rows] (MLP form)
+    unsigned long long *partial;  // {value, epoch} slots: [ns-1][B][rows]; MLP form [ns-1][gate, up][B][rows], then [ns-1][nbands][B] sums of x^2
     uint32_t epoch;
     uint32_t spin_limit;
     uint32_t rows, cols;
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     uint32_t *ldsM = reinterpret_cast<uint32_t *>(lds);  // [tr*16][Gp] s|b<<16, or [tr*16][Gp][2] f32
     unsigned char *img = lds + p.meta_bytes;              // [nT] tile images
     float *red = reinterpret_cast<float *>(lds + p.meta_bytes + p.img_bytes);
-    float *sq = red + p.tr * KW * B * 16u;  // MLP: [wave][B] partial sums of x^2 (finishers)
+    float *sq = red + p.tr * KW * B * 16u;  // MLP: [wave][B] sums of x^2 over the split's columns
 
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t *>(up_tile ? p.w2 : p.w), 0, int(p.w_bytes), kRsrcWord3);
@@ -208,8 +208,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
         load_x8(xv[i], xr, uint32_t(item_pos<B>(it).t), ST0 * kTileK + item_col<B>(it), p.cols, it < items);
     }
-    // MLP: the norm weights of the same columns, and in the finishers each
-    // x[t]'s sum of squares over all columns (for 1/rms at the end).
+    // MLP: the norm weights of the same columns.
     [[maybe_unused]] float nv[MLP ? XI : 1][8];
     if constexpr (MLP) {
         const __amdgpu_buffer_rsrc_t nr =
@@ -218,20 +217,6 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         for (int i = 0; i < XI; ++i) {
             const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
             load_x8(nv[i], nr, 0u, ST0 * kTileK + item_col<B>(it), p.cols, it < items);
-        }
-        if (finisher) {
-#pragma unroll
-            for (int t = 0; t < B; ++t) {
-                float v = 0.f;
-                for (uint32_t k = uint32_t(tid) * 4u; k < p.cols; k += uint32_t(nthr) * 4u) {
-                    const u4 q = __builtin_amdgcn_raw_buffer_load_b128(xr, int((uint32_t(t) * p.cols + k) * 4u), 0, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v += __uint_as_float(q[e]) * __uint_as_float(q[e]);
-                }
-#pragma unroll
-                for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-                if (lane == 0) sq[wave * B + t] = v;
-            }
         }
     }
 
@@ -323,15 +308,33 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     // ----
     u4 *imgA = reinterpret_cast<u4 *>(img);
     float4 *imgS = reinterpret_cast<float4 *>(img + nT * TIMG_A);
+    // MLP: each x[t]'s sum of squares over the split's columns, from the
+    // staged items (items past the split read zeros), for 1/rms at the end.
+    [[maybe_unused]] float xsq[MLP ? B : 1] = {};
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
         const uint32_t it = uint32_t(tid) + uint32_t(i * nthr);
         if (i > 0 && uint32_t(tid) - uint32_t(lane) + uint32_t(i * nthr) >= items) break;  // whole waves in or out
         if constexpr (MLP) {
+            float q = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q += xv[i][j] * xv[i][j];
+            const uint32_t it_t = item_pos<B>(it).t;
+#pragma unroll
+            for (int t = 0; t < B; ++t) xsq[t] += it_t == uint32_t(t) ? q : 0.f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) xv[i][j] *= nv[i][j];
         }
         stage_x_item<BITS, GROUP, B>(xv[i], it, it < items, lane, imgA, imgS);
+    }
+    if constexpr (MLP) {
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+            float v = xsq[t];
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+            if (lane == 0) sq[wave * B + t] = v;
+        }
     }
     // ---- 5. Metadata to LDS. ----
     if (vec_meta) {
@@ -503,8 +506,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const size_t stride = size_t(B) * p.rows;
     // Reads slot set k's value for oy once its epoch is this launch's;
     // past the host's spin limit it gives up (the caller writes NaN).
-    auto take = [&](uint32_t k, bool &ok) -> float {
-        unsigned long long *q = p.partial + size_t(k) * stride + oy;
+    auto take_at = [&](unsigned long long *q, bool &ok) -> float {
         unsigned long long word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (uint32_t spin = 0; uint32_t(word >> 32) != p.epoch; ++spin) {
             if (spin >= p.spin_limit) {
@@ -516,17 +518,27 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         }
         return __uint_as_float(uint32_t(word));
     };
-    auto publish = [&](uint32_t k, float value) {
+    auto take = [&](uint32_t k, bool &ok) -> float { return take_at(p.partial + size_t(k) * stride + oy, ok); };
+    auto publish_at = [&](unsigned long long *q, float value) {
         const unsigned long long word = (static_cast<unsigned long long>(p.epoch) << 32) | __float_as_uint(value);
-        __hip_atomic_store(p.partial + size_t(k) * stride + oy, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(q, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
+    auto publish = [&](uint32_t k, float value) { publish_at(p.partial + size_t(k) * stride + oy, value); };
     if constexpr (MLP) {
         // Slot sets [2*split] (gate) and [2*split + 1] (up) for splits
-        // 0..ns-2; the band's last split adds each in split order.
+        // 0..ns-2, then their sums of squares [split][band][B]; the band's
+        // last split adds each in split order.
         const float vu = wave_sum_of(tt + H);
+        float ss = 0.f;
+        for (uint32_t wv = 0; wv < p.tr * KW; ++wv) ss += sq[wv * B + t];
+        // Split k's sum of squares for this band and RHS (ns > 1 only).
+        auto sq_slot = [&](uint32_t k) {
+            return p.partial + size_t(2) * (p.ns - 1) * stride + (size_t(k) * p.nbands + band) * B + t;
+        };
         if (!finisher) {
             publish(2 * split, v);
             publish(2 * split + 1, vu);
+            if (tt == 0 && rr == 0) publish_at(sq_slot(split), ss);
             return;
         }
         bool ok = true;
@@ -539,9 +551,10 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
             }
             g = sg + v;
             u = su + vu;
+            float sx = take_at(sq_slot(0), ok);
+            for (uint32_t k = 1; k + 1 < p.ns; ++k) sx += take_at(sq_slot(k), ok);
+            ss = sx + ss;
         }
-        float ss = 0.f;
-        for (uint32_t wv = 0; wv < p.tr * KW; ++wv) ss += sq[wv * B + t];
         const float inv = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
         const float gn = g * inv;
         p.y[oy] = ok ? gn * (1.0f / (1.0f + expf(-gn))) * (u * inv) : __builtin_nanf("");
@@ -903,7 +916,9 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
 
 size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a) {
     if (pl.ns <= 1) return 0;
-    return size_t(pl.ns - 1) * (a.up_w ? 2 : 1) * a.batch * a.rows * sizeof(unsigned long long);
+    if (a.up_w)  // gate and up sums per row, then each band's sums of x^2
+        return size_t(pl.ns - 1) * (size_t(2) * a.rows + pl.nbands) * a.batch * sizeof(unsigned long long);
+    return size_t(pl.ns - 1) * a.batch * a.rows * sizeof(unsigned long long);
 }
 
 hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial, uint32_t epoch,
