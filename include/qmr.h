@@ -218,10 +218,13 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
 
 /* ---- Testing and tuning hooks (no counterpart in the reference). ---- */
 /* Force the GEMV kernel and tiling; 0,0 = planner (the row-band matrix-core
- * kernel where it has a one-round plan, else the split-K matrix-core kernel
- * where supported, the row-owning one past one round of resident workgroups
- * or for splits under four K tiles, else the vector-ALU kernels).
- *   rr = -3: row-owning matrix-core kernel (also the MLP form's); ks =
+ * kernel where it has a one-round plan, or, for matrices too tall for one
+ * round, single-split bands over several rounds; else the split-K
+ * matrix-core kernel where supported, the row-owning one past one round of
+ * resident workgroups or for splits under four K tiles, else the vector-ALU
+ * kernels). The fused MLP form: the row-band kernel's MLP form where it has
+ * a one-round plan, else split-K's, else the row-owning kernel's.
+ *   rr = -3: row-owning matrix-core kernel (also its MLP form); ks =
  *            j*10000 + rt*100 + kw pins its workgroup shape (rt row tiles x
  *            kw K waves) and, when j > 0, the entries per wave per staged
  *            chunk; 0 = its planner.
@@ -232,11 +235,10 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *            the row-slot tiling).
  *   rr > 0 with ks > 0: the vector-ALU row-slot kernel with `rr` rows per
  *            slot and a K-split of `ks`.
- *   rr = -4: row-band matrix-core kernel (the default where it has a plan
- *            whose workgroups are all resident at once); ks = ring*100000 +
- *            ns*10000 + tr*100 + kw pins its ring depth (2 or 3), K splits,
- *            row tiles per band and waves per tile; zero fields and ks = 0
- *            leave them to its planner.
+ *   rr = -4: row-band matrix-core kernel; ks = ring*100000 + ns*10000 +
+ *            tr*100 + kw pins its ring depth (2 or 3), K splits, row tiles
+ *            per band (the MLP form: tr/2 gate and tr/2 up tiles) and waves
+ *            per tile; zero fields and ks = 0 leave them to its planner.
  * Shapes a forced kernel does not support fall back to the next one; pairs
  * that are not compiled fall back to the planner. */
 int qmr_set_gemv_plan(qmr_device *device, int rr, int ks);
