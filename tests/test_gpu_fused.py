@@ -177,6 +177,27 @@ def test_matmul_affine_add_matches_product_plus_residual(gpu, rr, rows, cols, bi
         gpu.set_gemv_plan(0, 0)
 
 
+def test_residual_form_on_a_matrix_too_tall_for_one_round(gpu):
+    """y = r + W x where no row-band plan fits one round of resident
+    workgroups (about 1563 bands of 8 tiles): single-split bands over
+    several rounds, with a partial last tile and band, in place and into a
+    separate y, against the FP64 oracle."""
+    rows, cols, batch = 200003, 1024, 2
+    rng = np.random.default_rng(11)
+    m = _matrix(rng, rows, cols, 4, 64, "bf16")
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    r = rng.standard_normal((batch, rows)).astype(np.float32) * 10
+    want = oracle.matmul_add_f64(*m, "bf16", x, r, rows, cols, 4, 64, batch, 8)
+    gpu.set_gemv_plan(0, 0)
+    got, r_after = _run_add(gpu, m, x, r, rows, cols, 4, 64, batch, "bf16", in_place=False)
+    kernel = gpu.last_hip_kernel()
+    assert kernel.startswith("affine_band_kernel ring=") and kernel.endswith(" ns=1 tr=8 kw=1"), kernel
+    assert np.array_equal(r_after, r.ravel()), "the residual input was modified"
+    assert_gate(got, want, f"add {rows}x{cols} B{batch} multi-round")
+    got2, _ = _run_add(gpu, m, x, r, rows, cols, 4, 64, batch, "bf16", in_place=True)
+    assert np.array_equal(got2.view(np.uint32), got.view(np.uint32)), "in-place result differs"
+
+
 def test_fused_alias_rules_and_reference_mode(gpu):
     rows, cols = 64, 512
     rng = np.random.default_rng(1)
