@@ -37,7 +37,10 @@
 // launch's is complete, so one read both checks and fetches it, with no
 // counter and no fence chain. The sum is taken in split order, so results
 // do not depend on timing. The wait is bounded: past the host's spin limit
-// the workgroup writes NaN and exits, so every wave always finishes.
+// the workgroup writes NaN and exits, so every wave always finishes. The
+// planner takes split plans only when all their workgroups are resident at
+// once; single-split plans, in which no workgroup waits, may span several
+// rounds (matrices too tall for one).
 //
 // Build. This file is compiled once per weight format with
 // -DQMR_BAND_BITS=<4|8> -DQMR_BAND_META=<0|1|2>: each such object holds the
