@@ -246,6 +246,10 @@ def test_default_plan_kernel_family(gpu, rows, cols, bits, batch, kind):
     assert plan[0] == kind, f"{rows}x{cols} B{batch}: expected plan kind {kind}, got {plan}"
     if rows == 151936:
         assert plan[1] == (210801 if batch == 1 else 310801), plan
+    if rows == cols == 5120:
+        # Short streams (under 8 entries per wave) at one RHS take half-height
+        # bands; at three RHS the planner's own pick stands.
+        assert plan[1] // 100 % 100 == (2 if batch == 1 else 4), plan
 
 
 @pytest.mark.parametrize("rr,name,batch", [(0, "matmul_affine_bf16", 1), (0, "matmul_affine_bf16", 3),
