@@ -85,7 +85,7 @@ SETTLE_MS = 1000.0
 HOLD_US = 40  # GPU-side hold per timed launch, ahead of the start mark
 
 
-def settle(gpu: qmr.Gpu, name: str, bufsets, params, threads: int, ms: float) -> None:
+def settle(gpu: qmr.Gpu, name: str, bufsets, params, threads: int, ms: float, static: bool = False) -> None:
     """Untimed launches until about `ms` of GPU time has run. The clocks ramp
     up over a few hundred milliseconds of load after the host has kept the
     GPU idle (as it does while it builds each synthetic matrix): on MI355X
@@ -95,28 +95,30 @@ def settle(gpu: qmr.Gpu, name: str, bufsets, params, threads: int, ms: float) ->
     cmd = gpu.begin()
     a = cmd.mark()
     for k in range(10):
-        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128, static_scratch=static)
     b = cmd.mark()
     cmd.finish()
     per = max(cmd.elapsed_ms(a, b) / 10, 1e-3)
     cmd.release()
     cmd = gpu.begin()
     for k in range(int(ms / per)):
-        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128, static_scratch=static)
     cmd.finish()
     cmd.release()
 
 
-def time_kernel(gpu: qmr.Gpu, name: str, bufsets, params, steps: int, warmup: int):
+def time_kernel(gpu: qmr.Gpu, name: str, bufsets, params, steps: int, warmup: int, static: bool = False):
     """Back-to-back launch timing (events at both ends of the timed region),
     plus per-launch event brackets for the spread. Returns
     (mean ms per launch back-to-back, wall seconds of that region,
-     per-launch bracketed durations in ms)."""
+     per-launch bracketed durations in ms). `static` encodes through
+    qmr_encode_static (workspace in the static scratch)."""
     _, threads = qmr.dispatch_layout(name, params)
-    settle(gpu, name, bufsets, params, threads, SETTLE_MS)
+    settle(gpu, name, bufsets, params, threads, SETTLE_MS, static)
+    enc = lambda cmd, k: cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128, static_scratch=static)
     cmd = gpu.begin()
     for k in range(warmup):
-        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+        enc(cmd, k)
     cmd.finish()
     cmd.release()
     # Timed region: synchronised on both sides, K launches back to back. A
@@ -131,7 +133,7 @@ def time_kernel(gpu: qmr.Gpu, name: str, bufsets, params, steps: int, warmup: in
     t0 = time.perf_counter()
     a = cmd.mark()
     for k in range(steps):
-        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+        enc(cmd, k)
     b = cmd.mark()
     enqueue_us = (time.perf_counter() - t0) * 1e6
     cmd.finish()
@@ -151,7 +153,7 @@ def time_kernel(gpu: qmr.Gpu, name: str, bufsets, params, steps: int, warmup: in
     cmd.delay(min(HOLD_US * 3 * n, 1_000_000))
     for k in range(n):
         a = cmd.mark()
-        cmd.encode(name, bufsets[k % len(bufsets)], params, threads, 128)
+        enc(cmd, k)
         marks.append((a, cmd.mark()))
     cmd.finish()
     durs = [cmd.elapsed_ms(a, b) for a, b in marks]
@@ -568,6 +570,173 @@ def bench_block_vs_sequential(gpu: qmr.Gpu, iterations: int) -> dict:
     return r
 
 
+# Published results of the reference's kernel-bench on Apple M5 Pro
+# (docs/benchmarks/m5-pro-aligned-kernels-user.json), FP32 metadata.
+KERNEL_BENCH_PUBLISHED = {(17408, 5120): {"device": "Apple M5 Pro", "iterations": 100,
+                                          "milliseconds_per_matvec": 0.24718958,
+                                          "effective_weight_gb_per_second": 225.35577753722467},
+                          (248320, 5120): {"device": "Apple M5 Pro", "iterations": 12,
+                                           "milliseconds_per_matvec": 2.9875903333333333,
+                                           "effective_weight_gb_per_second": 265.97488656131014}}
+
+
+def kernel_bench(gpu: qmr.Gpu, rows: int, cols: int, iterations: int, bf16: bool, bits: int = 4,
+                 group: int = 64) -> dict:
+    """The reference's `kernel-bench` command (src/main.rs:552-644), same
+    method: every packed word 0x76543210, every scale 0.015625 and bias
+    -0.0625 (exact in BF16, so both metadata modes hold the same values),
+    x = 0.1; one weight copy; 3 warmup dispatches in one command, then
+    `iterations` dispatches of matvec_affine[_bf16] in one command, timed by
+    the host wall clock from the command's begin to its finish;
+    milliseconds_per_matvec and effective_weight_gb_per_second over the
+    code, scale and bias bytes. The same weights are read every time, so on
+    this device the matrix may be served from the 256 MB Infinity Cache (the
+    reference's own note says so for its cache); the rotating-copy metric
+    above is the one that excludes it."""
+    elements = rows * cols
+    w = np.full(elements // (32 // bits), 0x76543210, np.uint32)
+    sv = np.full(elements // group, 0.015625, np.float32)
+    bv = np.full(elements // group, -0.0625, np.float32)
+    if bf16:
+        sv, bv = synth.f32_to_bf16_bits(sv), synth.f32_to_bf16_bits(bv)
+    bufs = [gpu.upload_bytes(w), gpu.upload_bytes(sv), gpu.upload_bytes(bv),
+            gpu.upload_f32(np.full(cols, 0.1, np.float32)), gpu.alloc_f32(rows)]
+    name = "matvec_affine_bf16" if bf16 else "matvec_affine"
+    params = [rows, cols, bits, group]
+
+    def dispatch(count: int) -> float:
+        start = time.perf_counter()
+        cmd = gpu.begin()
+        for _ in range(count):
+            cmd.encode(name, bufs, params, rows * 32, 128)
+        cmd.finish()
+        cmd.release()
+        return time.perf_counter() - start
+
+    dispatch(3)
+    seconds = dispatch(iterations)
+    y = gpu.read_f32(bufs[4], rows)
+    if not np.isfinite(y).all():
+        raise RuntimeError("kernel-bench: non-finite kernel output")
+    # Every row is the same affine dot: sum over columns of (q*s + b)*0.1 with
+    # q cycling 0..7 (the word 0x76543210).
+    q = np.tile(np.arange(8, dtype=np.float64), cols // 8)
+    want = float(((q * 0.015625 - 0.0625) * np.float64(np.float32(0.1))).sum())
+    if not np.allclose(y, want, rtol=1e-5, atol=1e-5):
+        raise RuntimeError(f"kernel-bench: output {y[:4]} differs from {want}")
+    wbytes = sum(b.nbytes for b in (w, sv, bv))
+    r = {"kind": "packed_matvec_microbenchmark", "bits": bits, "group_size": group,
+         "kernel_mode": gpu.kernel_mode(), "metadata_mode": "bf16" if bf16 else "f32",
+         "synthetic_metadata_values": {"scale": 0.015625, "bias": -0.0625},
+         "device": gpu.name(), "rows": rows, "cols": cols, "iterations": iterations, "seconds": seconds,
+         "milliseconds_per_matvec": seconds * 1000.0 / iterations,
+         "effective_weight_gb_per_second": wbytes * iterations / seconds / 1e9,
+         "hip_launch": gpu.last_hip_kernel(),
+         "note": ("Repeated synthetic weights may benefit from cache (here the 256 MB Infinity Cache). "
+                  "This is NOT model tokens per second."),
+         "timing": "host wall clock from command begin to finish, as the reference's kernel-bench"}
+    pub = KERNEL_BENCH_PUBLISHED.get((rows, cols))
+    if pub and not bf16:
+        r["reference_published"] = pub
+    log(f"bench:   kernel-bench {rows}x{cols} {r['metadata_mode']} x{iterations}: "
+        f"{r['milliseconds_per_matvec'] * 1e3:.2f} us per matvec, "
+        f"{r['effective_weight_gb_per_second']:.1f} GB/s effective")
+    for b in bufs:
+        b.release()
+    return r
+
+
+def bench_kernel_bench(gpu: qmr.Gpu) -> list:
+    """kernel_bench at the reference's default shape (17408x5120, 50
+    iterations; its published run used 100), the metric's transpose and the
+    reference's large published shape, in both metadata modes."""
+    out = []
+    for rows, cols, iters in ((17408, 5120, 100), (5120, 17408, 100), (248320, 5120, 12)):
+        for bf16 in (False, True):
+            log(f"bench: kernel-bench {rows}x{cols} {'bf16' if bf16 else 'f32'} metadata, {iters} iterations")
+            out.append(kernel_bench(gpu, rows, cols, iters, bf16))
+    return out
+
+
+def bench_static_entry(gpu: qmr.Gpu, m: synth.PackedMatrix, mats, args) -> list:
+    """The metric GEMV and block through qmr_encode_static (every workspace
+    in the static scratch, nothing allocated) beside qmr_encode, timed the
+    same way: the row-band split sums then need no fill launch between
+    consecutive calls (the last splits clear the slots they take)."""
+    out = []
+    for batch in (1, 3):
+        x = synth.activations(m.cols, batch, synth.DEFAULT_SEED, tag="bench")
+        xb = gpu.upload_f32(x.ravel())
+        ys = [gpu.alloc_f32(batch * m.rows) for _ in mats]
+        bufsets = [[w, s, b, xb, y] for (w, s, b), y in zip(mats, ys)]
+        name = "matvec_affine_bf16" if batch == 1 else "matmul_affine_bf16"
+        params = [m.rows, m.cols, 4, 64] + ([batch] if batch > 1 else [])
+        log(f"bench: qmr_encode_static {m.rows}x{m.cols} B={batch}")
+        mean_ms, _, _ = time_kernel(gpu, name, bufsets, params, args.steps, args.warmup, static=True)
+        out.append({"shape": f"{m.rows}x{m.cols}", "batch": batch, "entry": "qmr_encode_static",
+                    "hip_launch": gpu.last_hip_kernel(), "us_mean": round(mean_ms * 1e3, 3),
+                    "gbps": round(synth.algorithmic_bytes(m, batch) / (mean_ms * 1e-3) / 1e9, 1)})
+        log(f"bench:   {out[-1]['us_mean']} us ({out[-1]['hip_launch']})")
+        del bufsets, ys, xb
+    return out
+
+
+def floor_sweep(gpu: qmr.Gpu, args) -> dict:
+    """read_checksum, the read floor, over sizes (25-500 MB, default
+    geometry) and over its geometry at the metric matrix's 50.1 MB
+    (workgroups, 16-byte loads in flight per thread, non-temporal or plain
+    loads). Each size splits into three views in the metric matrix's
+    proportions (codes, scales, biases); each case rotates over enough copies
+    to exceed the 256 MB Infinity Cache (at least 10, and at least 1 GB),
+    timed as the GEMV is."""
+    m = synth.q4_bf16_matrix(*synth.MLP_SHAPES["down"], synth.DEFAULT_SEED, tag="down")
+    frac = [m.w.nbytes / m.nbytes, m.s.nbytes / m.nbytes, m.b.nbytes / m.nbytes]
+    outs = [gpu.alloc_f32(qmr.CHECKSUM_SLOTS) for _ in range(2)]
+
+    def views(total: int, copies: int):
+        sizes = [int(total * f) // 16 * 16 for f in frac]
+        mats = [tuple(gpu.alloc_f32(n // 4) for n in sizes) for _ in range(copies)]
+        return sizes, mats
+
+    def run(sizes, mats, steps):
+        bufsets = [[a, b, c, outs[k % 2]] for k, (a, b, c) in enumerate(mats)]
+        mean_ms, _, durs = time_kernel(gpu, "read_checksum", bufsets, sizes, steps, 10)
+        return mean_ms, durs
+
+    res = {"sizes": [], "geometry": []}
+    for mb in (25, 50, 100, 200, 500):
+        total = m.nbytes * mb // 50
+        copies = max(10, -(-(1 << 30) // total))
+        sizes, mats = views(total, copies)
+        log(f"bench: floor sweep, {sum(sizes)} bytes, {copies} copies, default geometry")
+        mean_ms, durs = run(sizes, mats, max(40, min(args.steps, int(2e5 / mb))))
+        res["sizes"].append({"bytes": sum(sizes), "copies": copies, "us_mean": round(mean_ms * 1e3, 3),
+                             "us_p10_p50_p90": [round(v * 1e3, 3) for v in np.quantile(durs, [0.1, 0.5, 0.9])],
+                             "gbps": round(sum(sizes) / (mean_ms * 1e-3) / 1e9, 1)})
+        log(f"bench:   {res['sizes'][-1]['us_mean']} us, {res['sizes'][-1]['gbps']} GB/s")
+        for t in mats:
+            for b in t:
+                b.release()
+    sizes = [m.w.nbytes, m.s.nbytes, m.b.nbytes]
+    mats = [tuple(gpu.alloc_f32(n // 4) for n in sizes) for _ in range(10)]
+    for wg in (256, 512, 1024, 2048, 4080):
+        for unroll in (1, 2, 4, 8):
+            for nt in (1, 0):
+                if nt == 0 and unroll not in (4, 8):
+                    continue
+                gpu.set_read_plan(wg, unroll, nt)
+                mean_ms, durs = run(sizes, mats, args.steps)
+                res["geometry"].append({"workgroups": wg, "loads_in_flight_per_thread": unroll,
+                                        "kb_per_workgroup": round(sum(sizes) / wg / 1024, 1),
+                                        "nontemporal": bool(nt), "us_mean": round(mean_ms * 1e3, 3),
+                                        "gbps": round(sum(sizes) / (mean_ms * 1e-3) / 1e9, 1)})
+                log(f"bench:   floor geometry wg={wg} unroll={unroll} nt={nt}: {res['geometry'][-1]['us_mean']} us")
+    gpu.set_read_plan(0, 0, -1)
+    mean_ms, _ = run(sizes, mats, args.steps)
+    res["default_at_metric"] = {"bytes": sum(sizes), "us_mean": round(mean_ms * 1e3, 3)}
+    return res
+
+
 def read_floor(gpu: qmr.Gpu, m: synth.PackedMatrix, mats, args, steps: int = 0) -> dict:
     """The streaming-read floor of the metric launch: read_checksum (16-byte
     non-temporal loads over contiguous per-workgroup slices, XOR-reduced into
@@ -638,6 +807,10 @@ def main() -> int:
                          "e.g. -1,0 for the vector-ALU kernel (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run plain copies of MIB MiB (counter calibration for profiling)")
+    ap.add_argument("--no-kernel-bench", action="store_true",
+                    help="skip the reference's kernel-bench method (cache-warm host wall clock)")
+    ap.add_argument("--floor-sweep", action="store_true",
+                    help="only sweep read_checksum over sizes and geometries, print that JSON and exit")
     args = ap.parse_args()
     SETTLE_MS = args.settle_ms
     if args.gpus != 1:
@@ -655,12 +828,17 @@ def main() -> int:
         log(f"bench: forced GEMV plan ({rr}, {ks})")
     if args.copy_calibration:
         copy_calibration(gpu, args.copy_calibration, 8)
+    if args.floor_sweep:
+        print(json.dumps({"floor_sweep": floor_sweep(gpu, args)}), flush=True)
+        gpu.close()
+        return 0
     shapes = [] if args.only_wide else [("down", synth.MLP_SHAPES["down"])]
     if not args.only_metric and not args.only_wide:
         shapes.append(("gate_up", synth.MLP_SHAPES["gate_up"]))
     results = []
     metric_matrix = None
     floor = None
+    static_entry = []
     for tag, (rows, cols) in shapes:
         m = synth.q4_bf16_matrix(rows, cols, synth.DEFAULT_SEED, tag=tag)
         if tag == "down":
@@ -699,6 +877,8 @@ def main() -> int:
         if tag == "down":
             floor = read_floor(gpu, m, mats, args)
             log(f"bench:   read floor {floor['us_mean']} us ({floor['gbps']} GB/s)")
+            if not args.only_metric and not args.gemv_plan:
+                static_entry = bench_static_entry(gpu, m, mats, args)
         del mats
 
     if args.gemv_plan:
@@ -713,6 +893,7 @@ def main() -> int:
     dense = [] if (args.only_metric or args.no_dense) else bench_dense(gpu, args)
     loader = None if (args.only_metric or args.no_loader) else bench_loader(args)
     block_seq = None if (args.only_metric or args.block_iters <= 0) else bench_block_vs_sequential(gpu, args.block_iters)
+    kbench = [] if (args.only_metric or args.no_kernel_bench) else bench_kernel_bench(gpu)
     head = next(r for r in results if r["tag"] == "down" and r["batch"] == 1)
     b3 = next(r for r in results if r["tag"] == "down" and r["batch"] == 3)
     cpu = None
@@ -768,6 +949,8 @@ def main() -> int:
         "loader": loader,
         "wide": wide,
         "block_vs_sequential": block_seq,
+        "kernel_bench": kbench,
+        "static_entry": static_entry,
     }
     print(json.dumps(line), flush=True)
     gpu.close()

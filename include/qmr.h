@@ -137,7 +137,11 @@ int qmr_encode(qmr_command *command, const char *name, qmr_buffer *const *buffer
  * comes from a static scratch array of QMR_STATIC_SCRATCH_BYTES that each GPU
  * holds from library load until the process ends; a launch needing more is
  * rejected with QMR_ERR_INVALID before anything is enqueued. Workspace that
- * must start at zero is cleared by a fill kernel inside the call. All calls
+ * must start at zero is cleared by a fill kernel inside the call, except the
+ * row-band kernel's split sums of a GEMV or block (plain or residual form):
+ * its last splits clear every slot they take, so after the first fill the
+ * slots stay zero from call to call and need no fill until another path
+ * (split-K, wide, the MLP form) or a failed command has used them. All calls
  * on one GPU share its scratch: calls whose launches overlap in time (other
  * streams, other device handles on the same GPU) race. */
 #define QMR_STATIC_SCRATCH_BYTES (8u << 20)
@@ -248,6 +252,21 @@ int qmr_set_gemv_plan(qmr_device *device, int rr, int ks);
  * rr = -2 with ks = its K splits. */
 int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32_t bits,
                   uint32_t batch, int *rr, int *ks);
+/* Tuning hook for "read_checksum" (the read floor a product is measured
+ * against): workgroups of 256 threads (1..4096; 0 = about 48 KB each),
+ * 16-byte loads each thread keeps in flight (1, 2, 4 or 8; 0 = 4), and
+ * non-temporal (1) or plain (0) loads (-1 = the default, non-temporal). */
+int qmr_set_read_plan(qmr_device *device, uint32_t workgroups, uint32_t unroll, int nontemporal);
+/* Testing hook for the failure path of qmr_command_finish: while enabled,
+ * the row-band kernel's last K splits wait for sums that no split of the
+ * launch publishes and give up after a short bound (every workgroup still
+ * exits), as they would if a band's workgroups were not all resident at
+ * once; the command's finish then returns QMR_ERR_DEVICE naming the band. */
+int qmr_set_band_wait_fault(qmr_device *device, int enabled);
+/* Bytes of device workspace this handle has allocated for its kernels (the
+ * row-band split sums, the split-K partial sums and counters, the wide
+ * block's activation images); qmr_encode_static allocates none. */
+size_t qmr_device_workspace_bytes(const qmr_device *device);
 /* Reference pipeline label selected by the last successful qmr_encode. */
 const char *qmr_last_kernel(const qmr_device *device);
 /* The HIP kernel the last qmr_encode launched (with the row-band kernel's

@@ -79,8 +79,11 @@ struct BandParams {
     const float *norm;
     float eps;
     unsigned long long *partial;  // {value, epoch} slots: [ns-1][B][rows]; MLP form [ns-1][gate, up][B][rows], then [ns-1][nbands][B] sums of x^2
-    uint32_t epoch;
+    uint32_t epoch;       // tag of this launch's published sums
+    uint32_t wait_epoch;  // tag the last split waits for (the epoch; another value forces the give-up, for tests)
     uint32_t spin_limit;
+    uint32_t *status;     // set to 0x80000000 | band by a last split that gives up (may be null)
+    uint32_t reset_slots; // nonzero: the last split clears each slot it took (plain and residual forms)
     uint32_t rows, cols;
     uint32_t w_bytes, m_bytes;  // extents of the code and metadata views
     uint32_t tr, kw, ns, nbands;
@@ -508,10 +511,12 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const size_t oy = size_t(t) * p.rows + row;
     const size_t stride = size_t(B) * p.rows;
     // Reads slot set k's value for oy once its epoch is this launch's;
-    // past the host's spin limit it gives up (the caller writes NaN).
+    // past the host's spin limit it gives up: the caller writes NaN and
+    // reports the band in the status word, which the host turns into a
+    // failed command at its finish.
     auto take_at = [&](unsigned long long *q, bool &ok) -> float {
         unsigned long long word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (uint32_t spin = 0; uint32_t(word >> 32) != p.epoch; ++spin) {
+        for (uint32_t spin = 0; uint32_t(word >> 32) != p.wait_epoch; ++spin) {
             if (spin >= p.spin_limit) {
                 ok = false;
                 break;
@@ -522,6 +527,9 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         return __uint_as_float(uint32_t(word));
     };
     auto take = [&](uint32_t k, bool &ok) -> float { return take_at(p.partial + size_t(k) * stride + oy, ok); };
+    auto report = [&](bool ok) {
+        if (!ok && p.status) __hip_atomic_store(p.status, 0x80000000u | band, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    };
     auto publish_at = [&](unsigned long long *q, float value) {
         const unsigned long long word = (static_cast<unsigned long long>(p.epoch) << 32) | __float_as_uint(value);
         __hip_atomic_store(q, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -561,6 +569,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         const float inv = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
         const float gn = g * inv;
         p.y[oy] = ok ? gn * (1.0f / (1.0f + expf(-gn))) * (u * inv) : __builtin_nanf("");
+        report(ok);
         return;
     } else {
         if (p.ns > 1) {
@@ -569,24 +578,51 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
                 return;
             }
             // The band's last split: the other splits' sums, in split order.
+            // Each slot is this thread's alone, so with reset_slots it is
+            // cleared once taken, leaving the workspace zero for the next
+            // launch (which may then reuse the same epoch).
             bool ok = true;
             float sum = take(0, ok);
             for (uint32_t k = 1; k + 1 < p.ns; ++k) sum += take(k, ok);
+            if (p.reset_slots)
+                for (uint32_t k = 0; k + 1 < p.ns; ++k)
+                    __hip_atomic_store(p.partial + size_t(k) * stride + oy, 0ull, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
             v = ok ? sum + v : __builtin_nanf("");
+            report(ok);
         }
         p.y[oy] = FUSE == 1 ? p.r[oy] + v : v;
     }
 }
 
+// Raises a kernel's dynamic-LDS limit on the current device to `bytes`
+// (needed above 64 KB): once per kernel, device and larger size, under a
+// lock, so that device handles used from different threads do not race.
+hipError_t raise_lds_limit(const void *kernel, size_t bytes) {
+    static std::mutex mu;
+    static std::vector<std::pair<std::pair<const void *, int>, size_t>> done;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    for (auto &d : done) {
+        if (d.first.first != kernel || d.first.second != dev) continue;
+        if (d.second >= bytes) return hipSuccess;
+        e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+        if (e == hipSuccess) d.second = bytes;
+        return e;
+    }
+    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+    if (e == hipSuccess) done.push_back({{kernel, dev}, bytes});
+    return e;
+}
+
 template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE>
 hipError_t launch_inst(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
     auto kernel = affine_band_kernel<BITS, META, GROUP, B, XI, P, FUSE>;
-    static size_t configured = 0;
-    if (pl.lds > 65536 && pl.lds > configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(pl.lds));
+    if (pl.lds > 65536) {
+        const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kernel), pl.lds);
         if (e != hipSuccess) return e;
-        configured = pl.lds;
     }
     hipLaunchKernelGGL(kernel, dim3(pl.nbands * pl.ns), dim3(pl.tr * pl.kw * 64), pl.lds, stream, p);
     return hipGetLastError();
@@ -936,7 +972,7 @@ size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a) {
 }
 
 hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial, uint32_t epoch,
-                              hipStream_t stream) {
+                              const TileWait &wait, hipStream_t stream) {
     if (pl.kw == 0) return hipErrorInvalidValue;
     if (pl.ns > 1 && partial == nullptr) return hipErrorInvalidValue;
     BandParams p;
@@ -953,7 +989,12 @@ hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned 
     p.eps = a.eps;
     p.partial = partial;
     p.epoch = epoch;
-    p.spin_limit = 1u << 22;
+    // A forced give-up waits for a tag no split of this launch publishes,
+    // with a short bound, so that every workgroup still exits.
+    p.wait_epoch = wait.force_give_up ? epoch + 0x40000000u : epoch;
+    p.spin_limit = wait.force_give_up ? 64u : 1u << 22;
+    p.status = wait.status;
+    p.reset_slots = wait.reset_slots && a.up_w == nullptr ? 1u : 0u;
     p.rows = a.rows;
     p.cols = a.cols;
     p.w_bytes = uint32_t(uint64_t(a.rows) * a.cols * a.bits / 8);

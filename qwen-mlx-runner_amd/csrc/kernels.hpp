@@ -68,10 +68,18 @@ hipError_t launch_copy_f32(const float *x, float *y, uint32_t n, int num_cus, hi
 hipError_t launch_zero_u32(uint32_t *p, uint32_t n, hipStream_t stream);
 // One wave that returns after `ticks` of the device's real-time counter.
 hipError_t launch_delay(unsigned long long ticks, hipStream_t stream);
+// Geometry of read_checksum: workgroups of 256 threads (0 = about 48 KB per
+// workgroup), 16-byte loads per thread in flight (1, 2, 4 or 8; 0 = 4),
+// non-temporal loads (1), plain (0) or the default (-1: non-temporal).
+struct ReadPlan {
+    uint32_t workgroups = 0;
+    uint32_t unroll = 0;
+    int nt = -1;
+};
 // One streaming read of three views (byte sizes, multiples of 4); out holds
 // kChecksumSlots u32 whose XOR is the XOR of every word read.
 hipError_t launch_read_checksum(const void *a, uint32_t na, const void *b, uint32_t nb, const void *c, uint32_t nc,
-                                uint32_t *out, hipStream_t stream);
+                                uint32_t *out, const ReadPlan &plan, hipStream_t stream);
 // Streaming GEMV / small block on the matrix cores (batch 1..4; Q4/Q8;
 // group 32/64/128 with 2*batch <= 16*group/128). See affine_mfma.hip.
 struct MfmaPlan {
@@ -142,11 +150,25 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                           uint32_t force_tr = 0, uint32_t force_ns = 0, uint32_t force_ring = 0);
 // Workspace bytes for the partial-sum slots (0 when ns == 1).
 size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a);
-// `partial` holds affine_tile_workspace bytes (64-bit slots, any contents:
-// a slot counts only when its epoch matches); `epoch` must differ from the
-// previous launch's that used the same slots.
+// The last split's wait on the other splits' sums.
+struct TileWait {
+    // Device-visible word that a last split which gives up (its band's
+    // workgroups were not all resident) sets to 0x80000000 | band; null: no
+    // report (its outputs are NaN either way).
+    uint32_t *status = nullptr;
+    // The last split clears each slot it took (plain and residual forms), so
+    // that a workspace that was zero stays zero and the next launch may reuse
+    // the same epoch.
+    bool reset_slots = false;
+    // Testing: the last split waits for a tag no split publishes and gives up
+    // after a short bound; every workgroup still exits.
+    bool force_give_up = false;
+};
+// `partial` holds affine_tile_workspace bytes (64-bit slots: a slot counts
+// only when its epoch matches); `epoch` must differ from the previous
+// launch's that used the same slots, unless those slots were cleared.
 hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial,
-                              uint32_t epoch, hipStream_t stream);
+                              uint32_t epoch, const TileWait &wait, hipStream_t stream);
 
 // Wide block on MFMA (Q4/g64, F32 or BF16 metadata, batch up to 256): a prep
 // launch converts x into per-group images in `workspace` (wide_mfma_workspace

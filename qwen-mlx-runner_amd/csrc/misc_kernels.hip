@@ -329,14 +329,12 @@ __global__ __launch_bounds__(256) void copy_f32_kernel(const float *__restrict__
 // Pure streaming read of three views (sizes in bytes, multiples of 4). The
 // views' whole 16-byte chunks form one index space, cut into one contiguous
 // slice per workgroup; each thread requests U chunks at once with 16-byte
-// non-temporal loads (a view's chunk run may start at any 4-byte offset), so
-// a workgroup's slice, which may span two views, costs one memory round trip.
-// Slot g receives the XOR of workgroup g's words, the last workgroup also
-// reads the views' trailing (bytes % 16) / 4 words, and workgroup 0 zeroes
-// the slots past the grid. The shape measured fastest for one read of ~50 MB
-// on MI355X (back-to-back launches over rotating copies): ~4096 workgroups
-// of 256 threads, one slice each.
-template <int U>
+// loads (non-temporal when NT; a view's chunk run may start at any 4-byte
+// offset), so a workgroup's slice, which may span two views, costs one
+// memory round trip per U chunks per thread. Slot g receives the XOR of
+// workgroup g's words, the last workgroup also reads the views' trailing
+// (bytes % 16) / 4 words, and workgroup 0 zeroes the slots past the grid.
+template <int U, int NT>
 __global__ __launch_bounds__(256) void read_checksum_kernel(const unsigned char *a, uint32_t na,
                                                             const unsigned char *b, uint32_t nb,
                                                             const unsigned char *c, uint32_t nc, uint32_t *out,
@@ -354,7 +352,9 @@ __global__ __launch_bounds__(256) void read_checksum_kernel(const unsigned char 
             const unsigned char *p = kk < ca ? a + size_t(kk) * 16u
                                    : kk < cab ? b + size_t(kk - ca) * 16u
                                               : c + size_t(kk - cab) * 16u;
-            q[u] = kk < hi ? __builtin_nontemporal_load(reinterpret_cast<const copy_u4 *>(p)) : copy_u4{0, 0, 0, 0};
+            const copy_u4 *pv = reinterpret_cast<const copy_u4 *>(p);
+            if constexpr (NT != 0) q[u] = kk < hi ? __builtin_nontemporal_load(pv) : copy_u4{0, 0, 0, 0};
+            else q[u] = kk < hi ? *pv : copy_u4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) acc ^= q[u][0] ^ q[u][1] ^ q[u][2] ^ q[u][3];
@@ -378,15 +378,34 @@ __global__ __launch_bounds__(256) void read_checksum_kernel(const unsigned char 
 }  // namespace
 
 hipError_t launch_read_checksum(const void *a, uint32_t na, const void *b, uint32_t nb, const void *c, uint32_t nc,
-                                uint32_t *out, hipStream_t stream) {
+                                uint32_t *out, const ReadPlan &plan, hipStream_t stream) {
     const uint64_t total = uint64_t(na) + nb + nc;
-    // About 12 KB per workgroup (three 16-byte loads per thread), within
-    // [256, kChecksumSlots] workgroups.
-    uint64_t g = (total + 12287) / 12288;
-    g = g < 256 ? 256 : (g > kChecksumSlots ? kChecksumSlots : g);
-    hipLaunchKernelGGL(read_checksum_kernel<4>, dim3(uint32_t(g)), dim3(256), 0, stream,
-                       static_cast<const unsigned char *>(a), na, static_cast<const unsigned char *>(b), nb,
-                       static_cast<const unsigned char *>(c), nc, out, kChecksumSlots);
+    // Default: about 48 KB per workgroup (four 16-byte non-temporal loads per
+    // thread in flight), within [256, kChecksumSlots] workgroups. Measured on
+    // MI355X over the metric matrix's 50.1 MB (back-to-back launches over 10
+    // rotating copies): 1024 workgroups of 48 KB read it in 9.48-9.55 us,
+    // against 9.71-9.83 us for 4080 workgroups of 12 KB (the previous
+    // default), 11.6-11.8 us for 8160 and 15.3 us for 16320.
+    uint64_t g = plan.workgroups ? plan.workgroups : (total + 49151) / 49152;
+    if (!plan.workgroups && g < 256) g = 256;
+    g = g < 1 ? 1 : (g > kChecksumSlots ? kChecksumSlots : g);
+    const uint32_t u = plan.unroll ? plan.unroll : 4;
+    const bool nt = plan.nt >= 0 ? plan.nt != 0 : true;
+    auto *pa = static_cast<const unsigned char *>(a);
+    auto *pb = static_cast<const unsigned char *>(b);
+    auto *pc = static_cast<const unsigned char *>(c);
+    const dim3 grid{uint32_t(g)}, block{256u};
+    switch (u * 2 + (nt ? 1u : 0u)) {
+        case 2: hipLaunchKernelGGL((read_checksum_kernel<1, 0>), grid, block, 0, stream, pa, na, pb, nb, pc, nc, out, kChecksumSlots); break;
+        case 3: hipLaunchKernelGGL((read_checksum_kernel<1, 1>), grid, block, 0, stream, pa, na, pb, nb, pc, nc, out, kChecksumSlots); break;
+        case 4: hipLaunchKernelGGL((read_checksum_kernel<2, 0>), grid, block, 0, stream, pa, na, pb, nb, pc, nc, out, kChecksumSlots); break;
+        case 5: hipLaunchKernelGGL((read_checksum_kernel<2, 1>), grid, block, 0, stream, pa, na, pb, nb, pc, nc, out, kChecksumSlots); break;
+        case 8: hipLaunchKernelGGL((read_checksum_kernel<4, 0>), grid, block, 0, stream, pa, na, pb, nb, pc, nc, out, kChecksumSlots); break;
+        case 9: hipLaunchKernelGGL((read_checksum_kernel<4, 1>), grid, block, 0, stream, pa, na, pb, nb, pc, nc, out, kChecksumSlots); break;
+        case 16: hipLaunchKernelGGL((read_checksum_kernel<8, 0>), grid, block, 0, stream, pa, na, pb, nb, pc, nc, out, kChecksumSlots); break;
+        case 17: hipLaunchKernelGGL((read_checksum_kernel<8, 1>), grid, block, 0, stream, pa, na, pb, nb, pc, nc, out, kChecksumSlots); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

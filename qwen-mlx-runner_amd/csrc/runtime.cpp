@@ -8,9 +8,11 @@
 #include <atomic>
 #include <chrono>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <thread>
+#include <tuple>
 #include <unordered_map>
 #include <vector>
 
@@ -20,11 +22,15 @@
 
 using qmr::Error;
 
+// Everything a row-band plan depends on: rows, cols, bits, group, batch,
+// metadata format, MLP form, residual form, forced plan code, block schedule.
+using BandPlanKey = std::tuple<uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, int, bool, bool, int, int>;
+
 // Scratch of the no-allocation entry point (qmr_encode_static): a fixed array
 // in the code object, so that every GPU the library runs on holds its own
 // copy from module load until the process ends. On the host the array's name
 // is not a device address: host code reaches a GPU's copy only through the
-// address hipGetSymbolAddress returns with that GPU current (scratch_address
+// address hipGetSymbolAddress returns with that GPU current (scratch_entry
 // below, kept in qmr_device::scratch). Every qmr_encode_static call on a GPU
 // shares its copy, which keeps the last call's contents.
 static __device__ __align__(256) unsigned char scratch[QMR_STATIC_SCRATCH_BYTES];
@@ -60,15 +66,27 @@ struct qmr_device {
     unsigned long long *ws_slots = nullptr;
     size_t ws_slots_bytes = 0;
     uint32_t band_epoch = 0;
-    // Row-band plans by shape, format and forced plan: planning enumerates
-    // ~100 shapes with occupancy queries, which must not sit on every launch.
-    mutable std::unordered_map<uint64_t, qmr::TilePlan> band_plans;
+    // Row-band plans by shape, format, form, forced plan and block schedule:
+    // planning enumerates ~100 shapes with occupancy queries, which must not
+    // sit on every launch.
+    mutable std::map<BandPlanKey, qmr::TilePlan> band_plans;
     // Workspace of the wide-block kernel: the activation images.
     unsigned char *ws_wide = nullptr;
     size_t ws_wide_bytes = 0;
     // This GPU's copy of the static scratch (the workspace of
-    // qmr_encode_static, which allocates nothing).
+    // qmr_encode_static, which allocates nothing), and whether its row-band
+    // slot region is known to be all zero (shared by every handle on the GPU).
     unsigned char *scratch = nullptr;
+    std::atomic<bool> *scratch_clean = nullptr;
+    // Status word the row-band kernel sets when a last split gives up
+    // (host-coherent memory mapped into the device; read at finish), and its
+    // device address.
+    uint32_t *status_host = nullptr;
+    uint32_t *status_dev = nullptr;
+    // Testing hook: the row-band kernel's last splits give up (qmr_set_band_wait_fault).
+    bool force_give_up = false;
+    // Tuning hook: read_checksum's geometry (qmr_set_read_plan).
+    qmr::ReadPlan read_plan;
     // The open command whose start event is not recorded yet: it is recorded
     // on the stream just before the command's first launch (after any
     // workspace growth), so that a frame's GPU time starts when its GPU work
@@ -236,18 +254,25 @@ size_t pipeline_max_threads(const char *label) {
 
 // The device address of `scratch` on GPU `ordinal`, looked up once per GPU
 // with that GPU current (the caller has made it current) and kept for the
-// process, like the array itself.
-unsigned char *scratch_address(int ordinal) {
+// process, like the array itself; with it, the GPU's flag saying that the
+// scratch's row-band slot region is all zero (false until a fill kernel has
+// cleared it), shared by every device handle on that GPU.
+struct ScratchEntry {
+    unsigned char *address;
+    std::atomic<bool> *clean;
+};
+ScratchEntry scratch_entry(int ordinal) {
     static std::mutex mu;
-    static std::unordered_map<int, unsigned char *> addresses;
+    static std::unordered_map<int, ScratchEntry> entries;
     std::lock_guard<std::mutex> lock(mu);
-    const auto it = addresses.find(ordinal);
-    if (it != addresses.end()) return it->second;
+    const auto it = entries.find(ordinal);
+    if (it != entries.end()) return it->second;
     void *p = nullptr;
     check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (static scratch)");
     ensure(p != nullptr, "hipGetSymbolAddress returned no address for the static scratch", QMR_ERR_DEVICE);
-    addresses.emplace(ordinal, static_cast<unsigned char *>(p));
-    return static_cast<unsigned char *>(p);
+    const ScratchEntry e{static_cast<unsigned char *>(p), new std::atomic<bool>(false)};
+    entries.emplace(ordinal, e);
+    return e;
 }
 
 // qmr_encode_static runs only launches whose workspace fits the static
@@ -327,16 +352,14 @@ BandSchedule band_schedule(const qmr_device *dev) {
 // The row-band kernel's plan, honouring a forced shape (rr == -4, ks =
 // ring*100000 + ns*10000 + tr*100 + kw; zero fields leave them to its
 // planner) and the block schedule; a schedule's instance that has no
-// one-round plan runs the legacy plan.
+// one-round plan runs the legacy plan. Plans are cached under every field
+// they depend on.
 qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a,
                                BandSchedule sched = BandSchedule::Legacy) {
     const qmr::GemvPlan f = dev->forced_plan;
     const int ks = f.rr == -4 ? f.ks : 0;
-    uint64_t key = (uint64_t(a.rows) << 32) | a.cols;
-    key = key * 1000003u ^ (uint64_t(a.bits) << 24 | uint64_t(a.group) << 12 | uint64_t(a.batch) << 4 |
-                            uint64_t(static_cast<int>(a.meta)) << 2 | (a.up_w ? 2u : 0u) | (a.residual ? 1u : 0u));
-    key = key * 1000003u ^ uint64_t(uint32_t(ks));
-    key = key * 1000003u ^ uint64_t(static_cast<int>(sched));
+    const BandPlanKey key{a.rows, a.cols, a.bits, a.group, a.batch, static_cast<int>(a.meta), a.up_w != nullptr,
+                          a.residual != nullptr, ks, static_cast<int>(sched)};
     const auto it = dev->band_plans.find(key);
     if (it != dev->band_plans.end()) return it->second;
     qmr::TilePlan pl = sched != BandSchedule::Legacy ? forced_tile_plan(dev, a)
@@ -366,16 +389,33 @@ hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::Til
     const size_t need = qmr::affine_tile_workspace(pl, a);
     dev->last_hip = "affine_band_kernel ring=" + std::to_string(pl.ring) + " ns=" + std::to_string(pl.ns) +
                     " tr=" + std::to_string(pl.tr) + " kw=" + std::to_string(pl.kw);
+    qmr::TileWait wait;
+    wait.status = dev->status_dev;
+    wait.force_give_up = dev->force_give_up;
     if (fixed) {
-        // The static scratch holds whatever the last call left there: clear
-        // the slots (a fill kernel, so a captured graph clears them on every
-        // replay) and tag this launch's sums with epoch 1, which no cleared
-        // slot carries.
+        // The sums are tagged with epoch 1, which no cleared slot carries.
+        // The plain and residual forms' last splits clear each slot they
+        // take, so once the slot region is zero it stays zero from launch to
+        // launch and needs no fill; it is cleared (a fill kernel, so that a
+        // captured graph clears it on every replay) when it may hold other
+        // data: first use on this GPU, after the split-K or wide paths used
+        // the scratch, after an MLP form (whose slots are not cleared) and
+        // after a command that failed.
         check_static_scratch(need, "row-band split sums");
         start_gpu(dev);
-        const hipError_t e = qmr::launch_zero_u32(reinterpret_cast<uint32_t *>(fixed), uint32_t(need / 4), dev->stream);
-        if (e != hipSuccess) return e;
-        return qmr::launch_affine_tile(a, pl, reinterpret_cast<unsigned long long *>(fixed), 1u, dev->stream);
+        const bool plain = a.up_w == nullptr;
+        if (need > 0 && !dev->scratch_clean->load()) {
+            const hipError_t e =
+                qmr::launch_zero_u32(reinterpret_cast<uint32_t *>(fixed), uint32_t(need / 4), dev->stream);
+            if (e != hipSuccess) return e;
+        }
+        wait.reset_slots = plain;
+        const hipError_t e = qmr::launch_affine_tile(a, pl, reinterpret_cast<unsigned long long *>(fixed), 1u, wait,
+                                                     dev->stream);
+        // A region that was dirty is clean after the fill only if it covered
+        // all of it; ns == 1 plans touch no slot.
+        if (need > 0) dev->scratch_clean->store(plain && e == hipSuccess);
+        return e;
     }
     if (need > dev->ws_slots_bytes) {
         check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
@@ -394,7 +434,7 @@ hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::Til
         dev->band_epoch = 1;
     }
     start_gpu(dev);
-    return qmr::launch_affine_tile(a, pl, dev->ws_slots, dev->band_epoch, dev->stream);
+    return qmr::launch_affine_tile(a, pl, dev->ws_slots, dev->band_epoch, wait, dev->stream);
 }
 
 // Launch the split-K kernel with its partial sums and per-band arrival
@@ -411,6 +451,7 @@ hipError_t launch_split_k(qmr_device *dev, const qmr::AffineArgs &a, const qmr::
     const size_t part = (qmr::affine_mfma_workspace(pl, a) + 255) / 256 * 256;
     check_static_scratch(part + size_t(pl.nbands) * sizeof(uint32_t), "split-K partial sums and counters");
     uint32_t *counters = reinterpret_cast<uint32_t *>(fixed + part);
+    dev->scratch_clean->store(false);
     start_gpu(dev);
     const hipError_t e = qmr::launch_zero_u32(counters, pl.nbands, dev->stream);
     if (e != hipSuccess) return e;
@@ -515,8 +556,18 @@ int qmr_device_open(int ordinal, const qmr_device_options *options, qmr_device *
             check_hip(e, "hipStreamCreate");
         }
         try {
-            dev->scratch = scratch_address(ordinal);
+            const ScratchEntry se = scratch_entry(ordinal);
+            dev->scratch = se.address;
+            dev->scratch_clean = se.clean;
+            void *st = nullptr;
+            check_hip(hipHostMalloc(&st, 64, hipHostMallocMapped | hipHostMallocCoherent), "hipHostMalloc (status)");
+            dev->status_host = static_cast<uint32_t *>(st);
+            std::memset(st, 0, 64);
+            void *sd = nullptr;
+            check_hip(hipHostGetDevicePointer(&sd, st, 0), "hipHostGetDevicePointer (status)");
+            dev->status_dev = static_cast<uint32_t *>(sd);
         } catch (...) {
+            if (dev->status_host) hipHostFree(dev->status_host);
             hipStreamDestroy(dev->stream);
             delete dev;
             throw;
@@ -537,6 +588,7 @@ void qmr_device_close(qmr_device *device) {
     if (device->ws_wide) hipFree(device->ws_wide);
     if (device->ws_slots) hipFree(device->ws_slots);
     if (device->ws_counters) hipFree(device->ws_counters);
+    if (device->status_host) hipHostFree(device->status_host);
     for (int i = 0; i < 2; ++i) {
         if (device->pin[i]) hipHostFree(device->pin[i]);
         if (device->pin_done[i]) hipEventDestroy(device->pin_done[i]);
@@ -775,6 +827,21 @@ int qmr_command_finish(qmr_command *command, qmr_frame_timing *timing) {
         command->finished = true;
         if (e == hipSuccess) e = hipGetLastError();
         check_hip(e, "GPU command failed");
+        // A row-band launch of this command whose last split gave up waiting
+        // for its band's other splits (they were not all resident at once)
+        // wrote NaN for that band: the command failed, as a Metal command
+        // buffer whose status is not Completed does (src/gpu.rs:861-865).
+        // The static scratch may then hold sums that no launch cleared.
+        qmr_device *dev = command->device;
+        const uint32_t status = __atomic_load_n(dev->status_host, __ATOMIC_ACQUIRE);
+        if (status != 0) {
+            __atomic_store_n(dev->status_host, 0u, __ATOMIC_RELEASE);
+            dev->scratch_clean->store(false);
+            throw Error{QMR_ERR_DEVICE,
+                        "GPU command failed: affine_band_kernel band " + std::to_string(status & 0x7FFFFFFFu) +
+                            ": the last K split gave up waiting for the other splits' sums (the band's "
+                            "workgroups were not all resident at once); the command's outputs are not valid"};
+        }
         float ms = 0.f;
         check_hip(hipEventElapsedTime(&ms, command->marks[0], end), "hipEventElapsedTime");
         if (timing) {
@@ -920,7 +987,7 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
                                          reinterpret_cast<float *>(ptr(3)), dev->stream);
         } else if (name == "read_checksum") {
             e = qmr::launch_read_checksum(ptr(0), params[0], ptr(1), params[1], ptr(2), params[2],
-                                          reinterpret_cast<uint32_t *>(ptr(3)), dev->stream);
+                                          reinterpret_cast<uint32_t *>(ptr(3)), dev->read_plan, dev->stream);
         } else if (name == "copy_f32") {
             e = qmr::launch_copy_f32(reinterpret_cast<const float *>(ptr(0)),
                                      reinterpret_cast<float *>(ptr(1)), params[0], dev->limits.num_cus,
@@ -1015,7 +1082,10 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
             if (wide && qmr::wide_mfma_supported(a) && a.batch > 8) {
                 const size_t need = qmr::wide_mfma_workspace(a);
                 unsigned char *images = fixed;
-                if (fixed) check_static_scratch(need, "wide-block activation images");
+                if (fixed) {
+                    check_static_scratch(need, "wide-block activation images");
+                    dev->scratch_clean->store(false);
+                }
                 if (!fixed && need > dev->ws_wide_bytes) {
                     check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
                     if (dev->ws_wide) hipFree(dev->ws_wide);
@@ -1140,6 +1210,28 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group) {
 
 // ---- testing / tuning hooks (declared in include/qmr_tuning.h) ----
 
+int qmr_set_read_plan(qmr_device *device, uint32_t workgroups, uint32_t unroll, int nontemporal) {
+    return guarded([&]() -> int {
+        ensure(device != nullptr, "null device");
+        ensure(workgroups <= qmr::kChecksumSlots, "read_checksum: at most 4096 workgroups");
+        ensure(unroll == 0 || unroll == 1 || unroll == 2 || unroll == 4 || unroll == 8,
+               "read_checksum: loads in flight per thread must be 1, 2, 4 or 8 (0 = default)");
+        ensure(nontemporal >= -1 && nontemporal <= 1, "read_checksum: nontemporal must be -1, 0 or 1");
+        device->read_plan.workgroups = workgroups;
+        device->read_plan.unroll = unroll;
+        device->read_plan.nt = nontemporal;
+        return QMR_OK;
+    });
+}
+
+int qmr_set_band_wait_fault(qmr_device *device, int enabled) {
+    return guarded([&]() -> int {
+        ensure(device != nullptr, "null device");
+        device->force_give_up = enabled != 0;
+        return QMR_OK;
+    });
+}
+
 int qmr_set_gemv_plan(qmr_device *device, int rr, int ks) {
     return guarded([&]() -> int {
         ensure(device != nullptr, "null device");
@@ -1212,6 +1304,12 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
         if (ks) *ks = p.ks;
         return QMR_OK;
     });
+}
+
+size_t qmr_device_workspace_bytes(const qmr_device *device) {
+    if (!device) return 0;
+    return device->ws_slots_bytes + device->ws_partial_bytes + device->ws_counter_count * sizeof(uint32_t) +
+           device->ws_wide_bytes;
 }
 
 size_t qmr_device_max_lds(const qmr_device *device) {

@@ -48,7 +48,8 @@ EXPORTED_SYMBOLS = (
     "qmr_checked_buffer_range", "qmr_ranges_overlap", "qmr_specialized_matvec",
     "qmr_specialized_matmul", "qmr_parse_block_kernel_mode", "qmr_pack_bf16_exact",
     "qmr_supported_bf16_quantization", "qmr_set_gemv_plan", "qmr_gemv_plan", "qmr_wide_address_extent",
-    "qmr_last_kernel", "qmr_last_hip_kernel", "qmr_device_max_lds",
+    "qmr_last_kernel", "qmr_last_hip_kernel", "qmr_device_max_lds", "qmr_set_band_wait_fault",
+    "qmr_device_workspace_bytes", "qmr_set_read_plan",
     # include/qmr_checkpoint.h
     "qmr_checkpoint_open", "qmr_checkpoint_close", "qmr_checkpoint_tensor_count",
     "qmr_checkpoint_contains", "qmr_checkpoint_matrix_info", "qmr_checkpoint_matrix",
@@ -159,6 +160,9 @@ def lib() -> C.CDLL:
         "qmr_last_kernel": (C.c_char_p, [vp]),
         "qmr_last_hip_kernel": (C.c_char_p, [vp]),
         "qmr_device_max_lds": (sz, [vp]),
+        "qmr_set_band_wait_fault": (C.c_int, [vp, C.c_int]),
+        "qmr_device_workspace_bytes": (sz, [vp]),
+        "qmr_set_read_plan": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_int]),
         "qmr_checkpoint_open": (C.c_int, [C.c_char_p, C.POINTER(vp)]),
         "qmr_checkpoint_close": (None, [vp]),
         "qmr_checkpoint_tensor_count": (sz, [vp]),
@@ -390,6 +394,20 @@ class Gpu:
 
     def set_gemv_plan(self, rr: int = 0, ks: int = 0) -> None:
         _check(lib().qmr_set_gemv_plan(self._h, rr, ks))
+
+    def set_band_wait_fault(self, enabled: bool) -> None:
+        """Testing hook: the row-band kernel's last splits give up (their
+        command's finish then fails)."""
+        _check(lib().qmr_set_band_wait_fault(self._h, int(enabled)))
+
+    def set_read_plan(self, workgroups: int = 0, unroll: int = 0, nontemporal: int = -1) -> None:
+        """read_checksum's geometry (zeros and -1: the defaults)."""
+        _check(lib().qmr_set_read_plan(self._h, workgroups, unroll, nontemporal))
+
+    def workspace_bytes(self) -> int:
+        """Device workspace this handle has allocated (split sums, split-K
+        partials and counters, wide-block images)."""
+        return int(lib().qmr_device_workspace_bytes(self._h))
 
     def gemv_plan(self, rows: int, cols: int, bits: int, batch: int) -> tuple[int, int]:
         rr, ks = C.c_int(), C.c_int()

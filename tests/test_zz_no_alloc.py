@@ -88,12 +88,21 @@ CASES = [
 
 @pytest.mark.parametrize("form,plan,first,second,family", CASES)
 def test_static_entry_matches_qmr_encode_on_two_calls_in_a_row(gpu, form, plan, first, second, family):
+    """The static calls run on a device handle opened here, which has never
+    grown a workspace: after them it still holds none, so the calls could
+    only have used the static scratch. qmr_encode runs on the session handle."""
     rng = np.random.default_rng([len(form), *first, *second])
     cases = [_case(rng, form, *shape) for shape in (first, second)]
     static = []
-    for (rows, _, batch), (name, arrays, params, _) in zip((first, second), cases):
-        print(f"qmr_encode_static {name} {rows}x{params[1]} B={batch} plan {plan}", flush=True)
-        static.append(_launch(gpu, name, arrays, params, rows, batch, True, plan))
+    fresh = qmr.Gpu("aligned")
+    try:
+        assert fresh.workspace_bytes() == 0
+        for (rows, _, batch), (name, arrays, params, _) in zip((first, second), cases):
+            print(f"qmr_encode_static {name} {rows}x{params[1]} B={batch} plan {plan}", flush=True)
+            static.append(_launch(fresh, name, arrays, params, rows, batch, True, plan))
+        assert fresh.workspace_bytes() == 0, fresh.workspace_bytes()
+    finally:
+        fresh.close()
     # The first call takes a kernel with workspace (split sums when banded).
     kernel = static[0][1]
     assert kernel.startswith(family), (kernel, family)
@@ -106,6 +115,33 @@ def test_static_entry_matches_qmr_encode_on_two_calls_in_a_row(gpu, form, plan, 
         assert np.isfinite(got).all(), label
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), label
         assert_gate(got, want, label)
+
+
+def test_static_band_slots_stay_clear_across_a_sequence_of_calls(gpu):
+    """GEMVs and blocks on the row-band kernel clear the split-sum slots they
+    take, so consecutive static calls skip the fill; other paths (the MLP
+    form, split-K) leave the scratch to be cleared again. Every call of a
+    mixed sequence must match qmr_encode bit for bit."""
+    rng = np.random.default_rng(23)
+    seq = [("plain", (0, 0), (5120, 17408, 1)), ("plain", (0, 0), (5120, 17408, 3)),
+           ("residual", (0, 0), (2048, 8192, 2)), ("plain", (-4, 240202), (4096, 8192, 1)),
+           ("mlp", (0, 0), (1024, 2048, 2)), ("plain", (0, 0), (5120, 17408, 2)),
+           ("plain", (-2, 0), (4096, 2048, 1)), ("plain", (0, 0), (5120, 17408, 1)),
+           ("plain", (0, 0), (5120, 17408, 1))]
+    fresh = qmr.Gpu("aligned")
+    try:
+        for form, plan, (rows, cols, batch) in seq:
+            name, arrays, params, want = _case(rng, form, rows, cols, batch)
+            print(f"sequence: qmr_encode_static {name} {rows}x{cols} B={batch} plan {plan}", flush=True)
+            got, kernel = _launch(fresh, name, arrays, params, rows, batch, True, plan)
+            ref, ref_kernel = _launch(gpu, name, arrays, params, rows, batch, False, plan)
+            label = f"{form} {rows}x{cols} B={batch} ({kernel})"
+            assert kernel == ref_kernel, (kernel, ref_kernel)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), label
+            assert_gate(got, want, label)
+        assert fresh.workspace_bytes() == 0, fresh.workspace_bytes()
+    finally:
+        fresh.close()
 
 
 def test_static_entry_rejects_workspace_beyond_the_scratch(gpu):
