@@ -26,9 +26,10 @@ The CPU baseline times the FP64 oracle (the reference's per-weight
 dequantise-then-accumulate closure, restated in C) on this host.
 
 The read floor: read_checksum streams the metric matrix's codes, scales and
-biases (the same rotating copies, the same timing) and does nothing else; its
-time is reported as roofline.read_floor_us and roofline.frac_of_floor is that
-time over the GEMV's.
+biases (the same rotating copies, the same timing) and does nothing else, in
+three read geometries; the fastest is reported as roofline.read_floor_us and
+roofline.frac_of_floor is that time over the GEMV's. --floor-sweep sweeps it
+over sizes and geometries instead of running the bench.
 
 BASELINE config 3 (the Q8/g64 F16 5120x5120 projection, the same matrix with
 FP32 metadata, and the Q4/g64 BF16 151936x5120 vocabulary head, B=1 and B=3)
@@ -737,30 +738,47 @@ def floor_sweep(gpu: qmr.Gpu, args) -> dict:
     return res
 
 
+# read_checksum geometries (workgroups, 16-byte loads in flight per thread,
+# non-temporal) the floor takes the fastest of: the three fastest of the
+# geometry sweep at the metric matrix's 50 MB (profiles/read_checksum_floor_sweep.md),
+# whose order changes from box to box.
+FLOOR_GEOMETRIES = ((4080, 4, 1), (2048, 8, 1), (1024, 4, 1))
+
+
 def read_floor(gpu: qmr.Gpu, m: synth.PackedMatrix, mats, args, steps: int = 0) -> dict:
     """The streaming-read floor of the metric launch: read_checksum (16-byte
     non-temporal loads over contiguous per-workgroup slices, XOR-reduced into
     4096 slots) reads the same codes, scales and biases over the same
-    rotating copies, timed the same way as the GEMV. It does no arithmetic
-    beyond the XOR, so its time bounds what any kernel that reads these
-    bytes once can take on this device; the XOR of the slots is checked
-    against the host's XOR of every word."""
+    rotating copies, timed the same way as the GEMV, in each of
+    FLOOR_GEOMETRIES; the floor is the fastest. It does no arithmetic beyond
+    the XOR, so its time bounds what any kernel that reads these bytes once
+    can take on this device; the XOR of the slots is checked against the
+    host's XOR of every word."""
     outs = [gpu.alloc_f32(qmr.CHECKSUM_SLOTS) for _ in mats]
     bufsets = [[w, s, b, o] for (w, s, b), o in zip(mats, outs)]
     params = [m.w.nbytes, m.s.nbytes, m.b.nbytes]
-    log(f"bench: read floor, read_checksum of {m.nbytes} bytes ({len(mats)} rotating copies)")
-    mean_ms, _, durs = time_kernel(gpu, "read_checksum", bufsets, params, steps or args.steps, args.warmup)
     want = np.uint32(0)
     for a in (m.w, m.s, m.b):
         want ^= np.bitwise_xor.reduce(np.ascontiguousarray(a).view(np.uint32))
-    got = np.bitwise_xor.reduce(gpu.read_f32(outs[0], qmr.CHECKSUM_SLOTS).view(np.uint32))
-    if got != want:
-        raise RuntimeError(f"read_checksum XOR {got:#x} != host {want:#x}")
-    q = np.quantile(durs, [0.1, 0.5, 0.9])
-    return {"kernel": "read_checksum_kernel", "bytes": int(m.nbytes),
-            "us_mean": round(mean_ms * 1e3, 3),
-            "us_bracketed_p10_p50_p90": [round(v * 1e3, 3) for v in q],
-            "gbps": round(m.nbytes / (mean_ms * 1e-3) / 1e9, 1)}
+    runs = []
+    for wg, unroll, nt in FLOOR_GEOMETRIES:
+        gpu.set_read_plan(wg, unroll, nt)
+        log(f"bench: read floor, read_checksum of {m.nbytes} bytes ({len(mats)} rotating copies), "
+            f"{wg} workgroups x {unroll} loads in flight")
+        mean_ms, _, durs = time_kernel(gpu, "read_checksum", bufsets, params, steps or args.steps, args.warmup)
+        got = np.bitwise_xor.reduce(gpu.read_f32(outs[0], qmr.CHECKSUM_SLOTS).view(np.uint32))
+        if got != want:
+            raise RuntimeError(f"read_checksum XOR {got:#x} != host {want:#x}")
+        runs.append({"workgroups": wg, "loads_in_flight_per_thread": unroll, "nontemporal": bool(nt),
+                     "us_mean": round(mean_ms * 1e3, 3),
+                     "us_bracketed_p10_p50_p90": [round(v * 1e3, 3) for v in np.quantile(durs, [0.1, 0.5, 0.9])]})
+        log(f"bench:   {runs[-1]['us_mean']} us")
+    gpu.set_read_plan(0, 0, -1)
+    best = min(runs, key=lambda r: r["us_mean"])
+    return {"kernel": "read_checksum_kernel", "bytes": int(m.nbytes), "us_mean": best["us_mean"],
+            "geometry": {k: best[k] for k in ("workgroups", "loads_in_flight_per_thread", "nontemporal")},
+            "us_bracketed_p10_p50_p90": best["us_bracketed_p10_p50_p90"],
+            "gbps": round(m.nbytes / (best["us_mean"] * 1e-6) / 1e9, 1), "geometries": runs}
 
 
 def load_traffic(tag: str):
