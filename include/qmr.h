@@ -137,13 +137,15 @@ int qmr_encode(qmr_command *command, const char *name, qmr_buffer *const *buffer
  * comes from a static scratch array of QMR_STATIC_SCRATCH_BYTES that each GPU
  * holds from library load until the process ends; a launch needing more is
  * rejected with QMR_ERR_INVALID before anything is enqueued. Workspace that
- * must start at zero is cleared by a fill kernel inside the call, except the
- * row-band kernel's split sums of a GEMV or block (plain or residual form):
- * its last splits clear every slot they take, so after the first fill the
- * slots stay zero from call to call and need no fill until another path
- * (split-K, wide, the MLP form) or a failed command has used them. All calls
- * on one GPU share its scratch: calls whose launches overlap in time (other
- * streams, other device handles on the same GPU) race. */
+ * must start at zero (split sums tagged with a fixed epoch, arrival counters)
+ * is cleared by a fill kernel inside the call when earlier launches may have
+ * left it non-zero: the split-K kernel and the row-band kernel's GEMV and
+ * block forms (plain or residual) clear every slot and counter they take, so
+ * after the first fill the region stays zero from call to call and needs no
+ * fill until the wide block, the row-band MLP form or a failed command has
+ * used it. All calls on one GPU share its scratch: calls whose launches
+ * overlap in time (other streams, other device handles on the same GPU)
+ * race. */
 #define QMR_STATIC_SCRATCH_BYTES (8u << 20)
 int qmr_encode_static(qmr_command *command, const char *name, qmr_buffer *const *buffers,
                       const size_t *offsets, size_t nbuffers, const uint32_t *params,
@@ -258,10 +260,11 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
  * non-temporal (1) or plain (0) loads (-1 = the default, non-temporal). */
 int qmr_set_read_plan(qmr_device *device, uint32_t workgroups, uint32_t unroll, int nontemporal);
 /* Testing hook for the failure path of qmr_command_finish: while enabled,
- * the row-band kernel's last K splits wait for sums that no split of the
- * launch publishes and give up after a short bound (every workgroup still
- * exits), as they would if a band's workgroups were not all resident at
- * once; the command's finish then returns QMR_ERR_DEVICE naming the band. */
+ * the last K splits of the row-band and split-K kernels wait for sums that no
+ * split of the launch publishes and give up after a short bound (every
+ * workgroup still exits), as the row-band kernel's would if a band's
+ * workgroups were not all resident at once; the command's finish then
+ * returns QMR_ERR_DEVICE naming the kernel and band. */
 int qmr_set_band_wait_fault(qmr_device *device, int enabled);
 /* Bytes of device workspace this handle has allocated for its kernels (the
  * row-band split sums, the split-K partial sums and counters, the wide

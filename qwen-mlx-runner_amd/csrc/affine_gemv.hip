@@ -491,13 +491,9 @@ template <int BITS, int META, int B, int P, bool XLDS>
 hipError_t launch_units(const AffineArgs &a, hipStream_t stream, size_t lds_bytes, uint32_t group_shift,
                         uint32_t vec16, uint32_t rows_per_wg) {
     auto kernel = affine_gemv_units_kernel<BITS, META, B, P, XLDS>;
-    static size_t configured = 0;
-    if (lds_bytes > 65536 && lds_bytes > configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           int(lds_bytes));
+    if (lds_bytes > 65536) {
+        const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kernel), lds_bytes);
         if (e != hipSuccess) return e;
-        configured = lds_bytes;
     }
     const uint32_t blocks = (a.rows + rows_per_wg - 1) / rows_per_wg;
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kUThreads), lds_bytes, stream, a.w, a.s, a.b, a.x,
@@ -515,13 +511,9 @@ template <int BITS, int META, int B, int RR, int KS, bool XLDS>
 hipError_t launch_instance(const AffineArgs &a, hipStream_t stream, size_t lds_bytes,
                            uint32_t group_shift, uint32_t vec16) {
     auto kernel = affine_gemv_kernel<BITS, META, B, RR, KS, XLDS>;
-    static size_t configured = 0;
-    if (lds_bytes > 65536 && lds_bytes > configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           int(lds_bytes));
+    if (lds_bytes > 65536) {
+        const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kernel), lds_bytes);
         if (e != hipSuccess) return e;
-        configured = lds_bytes;
     }
     constexpr int kRowsPerWg = (kSlots / KS) * RR;
     const uint32_t blocks = (a.rows + kRowsPerWg - 1) / kRowsPerWg;

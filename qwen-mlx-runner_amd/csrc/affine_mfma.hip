@@ -32,9 +32,10 @@
 // and stages that range of x once in LDS, already split into hi/lo f16 in
 // MFMA operand order, with the per-group sums of x. A matrix is covered by
 // nbands x ns workgroups (row bands x K splits). With ns > 1 each workgroup
-// writes its partial sums to a workspace; the last workgroup of a band to
-// finish (an atomic counter) adds the ns partials in split order and writes
-// y, so results do not depend on timing. Each lane keeps P entries of loads
+// writes its partial sums to a workspace as 64-bit {value, epoch} slots; the
+// last workgroup of a band to finish (an atomic counter elects it) takes the
+// ns partials, each once its slot carries the launch's epoch, adds them in
+// split order and writes y, so results do not depend on timing. Each lane keeps P entries of loads
 // in flight in a register ring; the first P entries are requested before x is
 // staged.
 #include <hip/hip_runtime.h>
@@ -64,8 +65,8 @@ struct MfmaParams {
     const void *b;
     const float *x;
     float *y;
-    float *partial;      // [ns][B][rows] when ns > 1
-    uint32_t *counters;  // [nbands] when ns > 1, zero between launches
+    unsigned long long *slots;  // [mat][ns][B][rows] {value, epoch} when ns > 1 or MLP
+    uint32_t *counters;         // [nbands] when slots are used, zero between launches
     uint32_t rows, cols;
     uint32_t w_bytes, m_bytes;  // extents of the code and metadata views
     uint32_t nbands, ns, tiles, tps;
@@ -78,14 +79,16 @@ struct MfmaParams {
     const void *b2;
     const float *norm;
     float eps;
+    // Slot tags: partials are stored with `epoch`; the last arriver takes a
+    // slot once it carries `wait_epoch` (the same, except under the testing
+    // hook that forces a give-up), polling at most `spin_limit` times. A
+    // slot still untagged then leaves NaN for its output and sets `status`
+    // (0xC0000000 | band) for the host. With reset_slots the last arriver
+    // stores zero into every slot it took, so a zeroed region stays zeroed.
+    uint32_t epoch, wait_epoch, spin_limit;
+    uint32_t *status;
+    uint32_t reset_slots;
 };
-
-// This wave's earlier global writes complete before what follows (ahead of
-// the workgroup barrier that precedes a split's arrival).
-__device__ __forceinline__ void vmem_order() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
-}
 
 // FUSE 0: y = W x. FUSE 1: y = r + W x. FUSE 2: the fused MLP form. The
 // fused forms are separate instances so that the plain product's code is
@@ -327,24 +330,24 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
         }
         return;
     }
-    // Split K: publish this split's partial sums; the last workgroup of the
-    // band to arrive adds the ns partials in split order.
-    float *part = p.partial + size_t(mat * p.ns + split) * B * p.rows;
+    // Split K: publish this split's partial sums as {value, epoch} slots;
+    // the last workgroup of the band to arrive adds the ns partials in split
+    // order. The arrival counter only elects that workgroup: a partial counts
+    // once its slot's 64-bit word (one single-copy-atomic store) carries the
+    // launch's epoch, so the sum does not depend on when the other splits'
+    // stores become visible relative to their counter increments. Every
+    // other split incremented the counter after issuing its stores, so the
+    // last arriver's wait ends as soon as they land.
+    unsigned long long *part = p.slots + size_t(mat * p.ns + split) * B * p.rows;
+    const unsigned long long tag = (unsigned long long)p.epoch << 32;
     if (writer) {
-        if (t0 < B) __hip_atomic_store(part + size_t(t0) * p.rows + row, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t0 < B)
+            __hip_atomic_store(part + size_t(t0) * p.rows + row, tag | __float_as_uint(v0), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         if (t0 + 1 < B)
-            __hip_atomic_store(part + size_t(t0 + 1) * p.rows + row, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(part + size_t(t0 + 1) * p.rows + row, tag | __float_as_uint(v1), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
-    // Publication order without an agent-scope release or acquire (on gfx950
-    // these write back or invalidate the whole L2, which at the metric shape
-    // took the kernel from 15 to 37 us): the partials are agent-scope atomic
-    // stores, which the hardware writes through to the memory-side coherence
-    // point, and vmem_order waits until every one of them is acknowledged
-    // (vmcnt(0)) before the barrier; only then does thread 0 increment the
-    // band's counter. The last arriver reads the partials with agent-scope
-    // atomic loads, which bypass the non-coherent caches, after it has seen
-    // the final count, so each load returns the acknowledged value.
-    vmem_order();
     __syncthreads();
     if (tid == 0) {
         const uint32_t prev = __hip_atomic_fetch_add(&p.counters[band], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -352,8 +355,6 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
     }
     __syncthreads();
     if (*ldsLast == 0) return;
-    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     const uint32_t band_rows = RT * 16;
     // MLP: 1/rms of each x[t] (the staged x carried the norm weights only),
     // from sum(x^2) over all columns, reduced through LDS (the operand area
@@ -383,34 +384,49 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
             inv[t] = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
         }
     }
+    bool ok = true;
+    // The sum of one matrix's ns partials at slot `first` (stride apart), in
+    // split order: chunks of eight loads in flight, each slot polled until it
+    // carries the launch's epoch.
+    auto take = [&](unsigned long long *first, size_t stride) {
+        constexpr uint32_t kChunk = 8;
+        float v = 0.f;
+        for (uint32_t k0 = 0; k0 < p.ns; k0 += kChunk) {
+            unsigned long long w[kChunk];
+#pragma unroll
+            for (uint32_t k = 0; k < kChunk; ++k)
+                w[k] = k0 + k < p.ns ? __hip_atomic_load(first + (k0 + k) * stride, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT)
+                                     : 0ull;
+#pragma unroll
+            for (uint32_t k = 0; k < kChunk; ++k) {
+                if (k0 + k >= p.ns) break;
+                unsigned long long *slot = first + (k0 + k) * stride;
+                for (uint32_t spins = 0; uint32_t(w[k] >> 32) != p.wait_epoch;) {
+                    if (++spins > p.spin_limit) {
+                        ok = false;
+                        w[k] = 0x7FC00000ull;  // NaN
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                    w[k] = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                v += __uint_as_float(uint32_t(w[k]));
+                if (p.reset_slots) __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        return v;
+    };
+    const size_t stride = size_t(B) * p.rows;
     for (uint32_t i = tid; i < band_rows * B; i += nthr) {
         const uint32_t t = i / band_rows;
         const uint32_t rr = band_row0 + i % band_rows;
         if (rr >= p.rows) continue;
-        // All ns loads in flight at once, then added in split order.
-        float pv[kMaxSplits];
-        const float *pp = p.partial + size_t(t) * p.rows + rr;
-        const size_t stride = size_t(B) * p.rows;
-#pragma unroll
-        for (uint32_t k = 0; k < kMaxSplits; ++k) {
-            pv[k] = k < p.ns ? __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-            pp += stride;
-        }
-        float v = pv[0];
-#pragma unroll
-        for (uint32_t k = 1; k < kMaxSplits; ++k) v += pv[k];
         const size_t o = size_t(t) * p.rows + rr;
+        const float v = take(p.slots + o, stride);
         if constexpr (mlp) {
             // The up matrix's partials follow the gate's ns blocks.
-            const float *pu = p.partial + size_t(p.ns) * stride + size_t(t) * p.rows + rr;
-#pragma unroll
-            for (uint32_t k = 0; k < kMaxSplits; ++k) {
-                pv[k] = k < p.ns ? __hip_atomic_load(pu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-                pu += stride;
-            }
-            float u = pv[0];
-#pragma unroll
-            for (uint32_t k = 1; k < kMaxSplits; ++k) u += pv[k];
+            const float u = take(p.slots + size_t(p.ns) * stride + o, stride);
             float it = inv[0];
 #pragma unroll
             for (int tt = 1; tt < B; ++tt) it = uint32_t(tt) == t ? inv[tt] : it;
@@ -420,6 +436,8 @@ __global__ __launch_bounds__(kMaxRt * 64) void affine_mfma_kernel(MfmaParams p) 
             p.y[o] = FUSE == 1 ? p.r[o] + v : v;
         }
     }
+    if (!ok && p.status)
+        __hip_atomic_store(p.status, 0xC0000000u | band, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     if (tid == 0) __hip_atomic_store(&p.counters[band], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -431,12 +449,9 @@ hipError_t launch_b(const MfmaParams &p, uint32_t rt, size_t lds, hipStream_t st
     auto kernel = fuse == 2   ? affine_mfma_kernel<BITS, META, GROUP, B, kRing, PAIRS, 2>
                   : fuse == 1 ? affine_mfma_kernel<BITS, META, GROUP, B, kRing, PAIRS, 1>
                               : affine_mfma_kernel<BITS, META, GROUP, B, kRing, PAIRS, 0>;
-    static size_t configured[3] = {0, 0, 0};
-    if (lds > 65536 && lds > configured[fuse]) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (lds > 65536) {
+        const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kernel), lds);
         if (e != hipSuccess) return e;
-        configured[fuse] = lds;
     }
     hipLaunchKernelGGL(kernel, dim3(p.nbands * p.ns * (p.w2 ? 2u : 1u)), dim3(rt * 64), lds, stream, p);
     return hipGetLastError();
@@ -631,13 +646,13 @@ bool affine_mfma_supported(const AffineArgs &a) {
 
 size_t affine_mfma_workspace(const MfmaPlan &pl, const AffineArgs &a) {
     // The fused MLP form always publishes partials (gate and up meet in the
-    // band's last workgroup), one set per matrix.
+    // band's last workgroup), one set per matrix, as 64-bit slots.
     if (pl.ns <= 1 && !a.up_w) return 0;
-    return size_t(a.up_w ? 2 : 1) * pl.ns * a.batch * a.rows * sizeof(float);
+    return size_t(a.up_w ? 2 : 1) * pl.ns * a.batch * a.rows * sizeof(unsigned long long);
 }
 
-hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *partial,
-                              uint32_t *counters, hipStream_t stream) {
+hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, unsigned long long *slots,
+                              uint32_t *counters, uint32_t epoch, const TileWait &wait, hipStream_t stream) {
     MfmaParams p;
     p.w = a.w;
     p.s = a.s;
@@ -650,8 +665,13 @@ hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *pa
     p.b2 = a.up_b;
     p.norm = a.norm;
     p.eps = a.eps;
-    p.partial = partial;
+    p.slots = slots;
     p.counters = counters;
+    p.epoch = epoch;
+    p.wait_epoch = wait.force_give_up ? epoch + 0x40000000u : epoch;
+    p.spin_limit = wait.force_give_up ? 64u : 1u << 22;
+    p.status = wait.status;
+    p.reset_slots = wait.reset_slots ? 1u : 0u;
     p.rows = a.rows;
     p.cols = a.cols;
     p.w_bytes = uint32_t(uint64_t(a.rows) * a.cols * a.bits / 8);

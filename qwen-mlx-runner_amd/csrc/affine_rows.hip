@@ -402,13 +402,9 @@ template <int BITS, int META, int GROUP, int B, bool PAIRS>
 hipError_t launch_b(const RowsParams &p, uint32_t nbands, size_t lds, hipStream_t stream) {
     auto kernel = p.w2 ? affine_rows_kernel<BITS, META, GROUP, B, PAIRS, 1>
                        : affine_rows_kernel<BITS, META, GROUP, B, PAIRS, 0>;
-    static size_t configured[2] = {0, 0};
-    size_t &done = configured[p.w2 ? 1 : 0];
-    if (lds > 65536 && lds > done) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (lds > 65536) {
+        const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kernel), lds);
         if (e != hipSuccess) return e;
-        done = lds;
     }
     hipLaunchKernelGGL(kernel, dim3(nbands), dim3(p.rt * p.kw * 64), lds, stream, p);
     return hipGetLastError();

@@ -595,28 +595,6 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     }
 }
 
-// Raises a kernel's dynamic-LDS limit on the current device to `bytes`
-// (needed above 64 KB): once per kernel, device and larger size, under a
-// lock, so that device handles used from different threads do not race.
-hipError_t raise_lds_limit(const void *kernel, size_t bytes) {
-    static std::mutex mu;
-    static std::vector<std::pair<std::pair<const void *, int>, size_t>> done;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    std::lock_guard<std::mutex> lock(mu);
-    for (auto &d : done) {
-        if (d.first.first != kernel || d.first.second != dev) continue;
-        if (d.second >= bytes) return hipSuccess;
-        e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
-        if (e == hipSuccess) d.second = bytes;
-        return e;
-    }
-    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
-    if (e == hipSuccess) done.push_back({{kernel, dev}, bytes});
-    return e;
-}
-
 template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE>
 hipError_t launch_inst(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
     auto kernel = affine_band_kernel<BITS, META, GROUP, B, XI, P, FUSE>;

@@ -43,6 +43,12 @@ struct GemvPlan {
     int ks = 0;
 };
 
+// Raises a kernel's dynamic-LDS limit on the current device to `bytes`
+// (launches above 64 KB need it): once per kernel, device and larger size,
+// under a lock, so that device handles used from different threads do not
+// race on it.
+hipError_t raise_lds_limit(const void *kernel, size_t bytes);
+
 struct DeviceLimits {
     size_t max_lds_per_block;  // bytes of LDS one workgroup may allocate
     int num_cus;
@@ -80,6 +86,23 @@ struct ReadPlan {
 // kChecksumSlots u32 whose XOR is the XOR of every word read.
 hipError_t launch_read_checksum(const void *a, uint32_t na, const void *b, uint32_t nb, const void *c, uint32_t nc,
                                 uint32_t *out, const ReadPlan &plan, hipStream_t stream);
+// A last arriver's wait on the other K splits' {value, epoch} slots (the
+// row-band and split-K kernels).
+struct TileWait {
+    // Device-visible word that a last arriver which gives up sets to
+    // 0x80000000 | band (row-band kernel: its band's workgroups were not all
+    // resident) or 0xC0000000 | band (split-K kernel); null: no report (the
+    // outputs are NaN either way).
+    uint32_t *status = nullptr;
+    // The last arriver clears each slot it took (row-band: plain and residual
+    // forms; split-K: every form), so that a workspace that was zero stays
+    // zero and the next launch may reuse the same epoch.
+    bool reset_slots = false;
+    // Testing: the last arriver waits for a tag no split publishes and gives
+    // up after a short bound; every workgroup still exits.
+    bool force_give_up = false;
+};
+
 // Streaming GEMV / small block on the matrix cores (batch 1..4; Q4/Q8;
 // group 32/64/128 with 2*batch <= 16*group/128). See affine_mfma.hip.
 struct MfmaPlan {
@@ -97,10 +120,12 @@ bool affine_mfma_supported(const AffineArgs &a);
 MfmaPlan plan_affine_mfma(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_ns = 0);
 // Workspace bytes the plan needs for cross-workgroup partial sums (0 if none).
 size_t affine_mfma_workspace(const MfmaPlan &pl, const AffineArgs &a);
-// `partial` holds affine_mfma_workspace bytes; `counters` holds pl.nbands
-// zeroed u32 (the kernel returns them to zero).
-hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, float *partial,
-                              uint32_t *counters, hipStream_t stream);
+// `slots` holds affine_mfma_workspace bytes (64-bit slots: a partial counts
+// only when its epoch matches); `epoch` must differ from the previous
+// launch's that used the same slots, unless those slots were cleared;
+// `counters` holds pl.nbands zeroed u32 (the kernel returns them to zero).
+hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, unsigned long long *slots,
+                              uint32_t *counters, uint32_t epoch, const TileWait &wait, hipStream_t stream);
 
 // Streaming GEMV / small block on the matrix cores with every workgroup
 // owning whole rows (no cross-workgroup reduction). See affine_rows.hip.
@@ -150,20 +175,6 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                           uint32_t force_tr = 0, uint32_t force_ns = 0, uint32_t force_ring = 0);
 // Workspace bytes for the partial-sum slots (0 when ns == 1).
 size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a);
-// The last split's wait on the other splits' sums.
-struct TileWait {
-    // Device-visible word that a last split which gives up (its band's
-    // workgroups were not all resident) sets to 0x80000000 | band; null: no
-    // report (its outputs are NaN either way).
-    uint32_t *status = nullptr;
-    // The last split clears each slot it took (plain and residual forms), so
-    // that a workspace that was zero stays zero and the next launch may reuse
-    // the same epoch.
-    bool reset_slots = false;
-    // Testing: the last split waits for a tag no split publishes and gives up
-    // after a short bound; every workgroup still exits.
-    bool force_give_up = false;
-};
 // `partial` holds affine_tile_workspace bytes (64-bit slots: a slot counts
 // only when its epoch matches); `epoch` must differ from the previous
 // launch's that used the same slots, unless those slots were cleared.

@@ -54,18 +54,16 @@ struct qmr_device {
     qmr::GemvPlan forced_plan;
     std::string last_kernel;    // selected reference pipeline label
     std::string last_hip;       // HIP kernel (and plan) of the last launch
-    // Workspace of the split-K matrix-core kernel's cross-workgroup reduction:
-    // partial sums and per-band arrival counters (kept zero between launches).
-    float *ws_partial = nullptr;
-    size_t ws_partial_bytes = 0;
+    // Per-band arrival counters of the split-K matrix-core kernel (kept zero
+    // between launches).
     uint32_t *ws_counters = nullptr;
     size_t ws_counter_count = 0;
-    // Workspace of the row-band kernel's split sums: 64-bit {value, epoch}
-    // slots (contents need no clearing: a slot counts only when its epoch is
-    // the launch's), and the epoch of the last launch.
+    // Workspace of the row-band and split-K kernels' partial sums: 64-bit
+    // {value, epoch} slots (contents need no clearing: a slot counts only
+    // when its epoch is the launch's), and the epoch of the last launch.
     unsigned long long *ws_slots = nullptr;
     size_t ws_slots_bytes = 0;
-    uint32_t band_epoch = 0;
+    uint32_t slot_epoch = 0;
     // Row-band plans by shape, format, form, forced plan and block schedule:
     // planning enumerates ~100 shapes with occupancy queries, which must not
     // sit on every launch.
@@ -74,10 +72,10 @@ struct qmr_device {
     unsigned char *ws_wide = nullptr;
     size_t ws_wide_bytes = 0;
     // This GPU's copy of the static scratch (the workspace of
-    // qmr_encode_static, which allocates nothing), and whether its row-band
-    // slot region is known to be all zero (shared by every handle on the GPU).
+    // qmr_encode_static, which allocates nothing), and how many of its
+    // leading bytes may be non-zero (shared by every handle on the GPU).
     unsigned char *scratch = nullptr;
-    std::atomic<bool> *scratch_clean = nullptr;
+    std::atomic<size_t> *scratch_dirty = nullptr;
     // Status word the row-band kernel sets when a last split gives up
     // (host-coherent memory mapped into the device; read at finish), and its
     // device address.
@@ -225,6 +223,25 @@ int upload_staged(::qmr_device *device, const void *src, size_t bytes, ::qmr_buf
     });
 }
 
+hipError_t raise_lds_limit(const void *kernel, size_t bytes) {
+    static std::mutex mu;
+    static std::vector<std::pair<std::pair<const void *, int>, size_t>> done;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    for (auto &d : done) {
+        if (d.first.first != kernel || d.first.second != dev) continue;
+        if (d.second >= bytes) return hipSuccess;
+        e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+        if (e == hipSuccess) d.second = bytes;
+        return e;
+    }
+    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+    if (e == hipSuccess) done.push_back({{kernel, dev}, bytes});
+    return e;
+}
+
 size_t device_free_bytes(const ::qmr_device *device) {
     size_t free_bytes = 0, total = 0;
     check_hip(hipSetDevice(device->ordinal), "hipSetDevice");
@@ -254,12 +271,12 @@ size_t pipeline_max_threads(const char *label) {
 
 // The device address of `scratch` on GPU `ordinal`, looked up once per GPU
 // with that GPU current (the caller has made it current) and kept for the
-// process, like the array itself; with it, the GPU's flag saying that the
-// scratch's row-band slot region is all zero (false until a fill kernel has
+// process, like the array itself; with it, the GPU's count of the scratch's
+// leading bytes that may be non-zero (all of it until a fill kernel has
 // cleared it), shared by every device handle on that GPU.
 struct ScratchEntry {
     unsigned char *address;
-    std::atomic<bool> *clean;
+    std::atomic<size_t> *dirty;
 };
 ScratchEntry scratch_entry(int ordinal) {
     static std::mutex mu;
@@ -270,7 +287,7 @@ ScratchEntry scratch_entry(int ordinal) {
     void *p = nullptr;
     check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (static scratch)");
     ensure(p != nullptr, "hipGetSymbolAddress returned no address for the static scratch", QMR_ERR_DEVICE);
-    const ScratchEntry e{static_cast<unsigned char *>(p), new std::atomic<bool>(false)};
+    const ScratchEntry e{static_cast<unsigned char *>(p), new std::atomic<size_t>(QMR_STATIC_SCRATCH_BYTES)};
     entries.emplace(ordinal, e);
     return e;
 }
@@ -284,18 +301,53 @@ void check_static_scratch(size_t need, const char *what) {
                " (use qmr_encode, which grows its workspace)");
 }
 
-// Grow the device workspace (synchronising the stream before an old buffer
-// is freed, since queued launches may still use it).
-void ensure_workspace(qmr_device *dev, size_t partial_bytes, size_t counters) {
-    if (partial_bytes > dev->ws_partial_bytes) {
-        check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
-        if (dev->ws_partial) hipFree(dev->ws_partial);
-        dev->ws_partial = nullptr;
-        dev->ws_partial_bytes = 0;
-        size_t n = partial_bytes < (size_t(1) << 20) ? (size_t(1) << 20) : partial_bytes;
-        check_hip(hipMalloc(&dev->ws_partial, n), "hipMalloc (workspace)");
-        dev->ws_partial_bytes = n;
+// The static scratch's first `need` bytes, zeroed for a launch that tags its
+// slots with epoch 1: a fill kernel (so that a captured graph clears them on
+// every replay) clears everything earlier launches may have left non-zero.
+hipError_t clear_static_slots(qmr_device *dev, unsigned char *fixed, size_t need) {
+    const size_t dirty = dev->scratch_dirty->load();
+    if (need == 0 || dirty == 0) return hipSuccess;
+    const size_t n = (need > dirty ? need : dirty) / 4;
+    const hipError_t e = qmr::launch_zero_u32(reinterpret_cast<uint32_t *>(fixed), uint32_t(n), dev->stream);
+    if (e == hipSuccess) dev->scratch_dirty->store(0);
+    return e;
+}
+
+// Record that a launch may have left the static scratch's first `extent`
+// bytes non-zero.
+void mark_static_dirty(qmr_device *dev, size_t extent) {
+    size_t cur = dev->scratch_dirty->load();
+    while (cur < extent && !dev->scratch_dirty->compare_exchange_weak(cur, extent)) {
     }
+}
+
+// The device's slot workspace, grown to `need` bytes (after the stream
+// drains, since queued launches may use the old one), and the epoch of a new
+// launch that uses it. When the epoch wraps, the slots are cleared so that no
+// stale slot can carry the new epoch.
+uint32_t next_slot_epoch(qmr_device *dev, size_t need) {
+    if (need > dev->ws_slots_bytes) {
+        check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+        if (dev->ws_slots) hipFree(dev->ws_slots);
+        dev->ws_slots = nullptr;
+        dev->ws_slots_bytes = 0;
+        const size_t n = need < (size_t(1) << 20) ? (size_t(1) << 20) : need;
+        check_hip(hipMalloc(&dev->ws_slots, n), "hipMalloc (slot workspace)");
+        check_hip(hipMemsetAsync(dev->ws_slots, 0, n, dev->stream), "hipMemsetAsync (slot workspace)");
+        dev->ws_slots_bytes = n;
+    }
+    if (++dev->slot_epoch == 0) {
+        if (dev->ws_slots)
+            check_hip(hipMemsetAsync(dev->ws_slots, 0, dev->ws_slots_bytes, dev->stream),
+                      "hipMemsetAsync (slot workspace)");
+        dev->slot_epoch = 1;
+    }
+    return dev->slot_epoch;
+}
+
+// Grow the split-K arrival counters (synchronising the stream before an old
+// buffer is freed, since queued launches may still use it).
+void ensure_counters(qmr_device *dev, size_t counters) {
     if (counters > dev->ws_counter_count) {
         check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
         if (dev->ws_counters) hipFree(dev->ws_counters);
@@ -380,10 +432,8 @@ qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a,
     return pl;
 }
 
-// Launch the row-band kernel: grow the slot workspace when needed (after the
-// stream drains, since queued launches may use the old one) and advance the
-// launch epoch. When the epoch wraps, the slots are cleared so that no stale
-// slot can carry the new epoch.
+// Launch the row-band kernel over the device's slot workspace, or with
+// `fixed` (qmr_encode_static) over the static scratch.
 hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::TilePlan &pl,
                        unsigned char *fixed) {
     const size_t need = qmr::affine_tile_workspace(pl, a);
@@ -396,66 +446,54 @@ hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::Til
         // The sums are tagged with epoch 1, which no cleared slot carries.
         // The plain and residual forms' last splits clear each slot they
         // take, so once the slot region is zero it stays zero from launch to
-        // launch and needs no fill; it is cleared (a fill kernel, so that a
-        // captured graph clears it on every replay) when it may hold other
-        // data: first use on this GPU, after the split-K or wide paths used
-        // the scratch, after an MLP form (whose slots are not cleared) and
-        // after a command that failed.
+        // launch and needs no fill; it is cleared when earlier launches may
+        // have left it non-zero: first use on this GPU, after the split-K or
+        // wide paths used the scratch, after an MLP form (whose slots are
+        // not cleared) and after a command that failed.
         check_static_scratch(need, "row-band split sums");
         start_gpu(dev);
         const bool plain = a.up_w == nullptr;
-        if (need > 0 && !dev->scratch_clean->load()) {
-            const hipError_t e =
-                qmr::launch_zero_u32(reinterpret_cast<uint32_t *>(fixed), uint32_t(need / 4), dev->stream);
-            if (e != hipSuccess) return e;
-        }
+        hipError_t e = clear_static_slots(dev, fixed, need);
+        if (e != hipSuccess) return e;
         wait.reset_slots = plain;
-        const hipError_t e = qmr::launch_affine_tile(a, pl, reinterpret_cast<unsigned long long *>(fixed), 1u, wait,
-                                                     dev->stream);
-        // A region that was dirty is clean after the fill only if it covered
-        // all of it; ns == 1 plans touch no slot.
-        if (need > 0) dev->scratch_clean->store(plain && e == hipSuccess);
+        e = qmr::launch_affine_tile(a, pl, reinterpret_cast<unsigned long long *>(fixed), 1u, wait, dev->stream);
+        if (!plain || e != hipSuccess) mark_static_dirty(dev, need);
         return e;
     }
-    if (need > dev->ws_slots_bytes) {
-        check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
-        if (dev->ws_slots) hipFree(dev->ws_slots);
-        dev->ws_slots = nullptr;
-        dev->ws_slots_bytes = 0;
-        const size_t n = need < (size_t(1) << 20) ? (size_t(1) << 20) : need;
-        check_hip(hipMalloc(&dev->ws_slots, n), "hipMalloc (band workspace)");
-        check_hip(hipMemsetAsync(dev->ws_slots, 0, n, dev->stream), "hipMemsetAsync (band workspace)");
-        dev->ws_slots_bytes = n;
-    }
-    if (++dev->band_epoch == 0) {
-        if (dev->ws_slots)
-            check_hip(hipMemsetAsync(dev->ws_slots, 0, dev->ws_slots_bytes, dev->stream),
-                      "hipMemsetAsync (band workspace)");
-        dev->band_epoch = 1;
-    }
+    const uint32_t epoch = next_slot_epoch(dev, need);
     start_gpu(dev);
-    return qmr::launch_affine_tile(a, pl, dev->ws_slots, dev->band_epoch, wait, dev->stream);
+    return qmr::launch_affine_tile(a, pl, dev->ws_slots, epoch, wait, dev->stream);
 }
 
-// Launch the split-K kernel with its partial sums and per-band arrival
-// counters: the device's growable workspace, or with `fixed` (qmr_encode_static)
-// the static scratch, whose counters a fill kernel clears first (the kernel
-// needs them zero; partial sums are written before they are read).
+// Launch the split-K kernel with its partial-sum slots and per-band arrival
+// counters: the device's workspaces, or with `fixed` (qmr_encode_static) the
+// static scratch (slots, then counters), zeroed where earlier launches may
+// have left data; its last arrivers clear every slot they take and their
+// counters, so a successful launch leaves the region zero.
 hipError_t launch_split_k(qmr_device *dev, const qmr::AffineArgs &a, const qmr::MfmaPlan &pl,
                           unsigned char *fixed) {
+    qmr::TileWait wait;
+    wait.status = dev->status_dev;
+    wait.force_give_up = dev->force_give_up;
+    const size_t need = qmr::affine_mfma_workspace(pl, a);
     if (!fixed) {
-        ensure_workspace(dev, qmr::affine_mfma_workspace(pl, a), pl.nbands);
+        const uint32_t epoch = next_slot_epoch(dev, need);
+        ensure_counters(dev, pl.nbands);
         start_gpu(dev);
-        return qmr::launch_affine_mfma(a, pl, dev->ws_partial, dev->ws_counters, dev->stream);
+        return qmr::launch_affine_mfma(a, pl, dev->ws_slots, dev->ws_counters, epoch, wait, dev->stream);
     }
-    const size_t part = (qmr::affine_mfma_workspace(pl, a) + 255) / 256 * 256;
-    check_static_scratch(part + size_t(pl.nbands) * sizeof(uint32_t), "split-K partial sums and counters");
+    const size_t part = (need + 255) / 256 * 256;
+    const size_t extent = part + size_t(pl.nbands) * sizeof(uint32_t);
+    check_static_scratch(extent, "split-K partial sums and counters");
     uint32_t *counters = reinterpret_cast<uint32_t *>(fixed + part);
-    dev->scratch_clean->store(false);
     start_gpu(dev);
-    const hipError_t e = qmr::launch_zero_u32(counters, pl.nbands, dev->stream);
+    hipError_t e = clear_static_slots(dev, fixed, (extent + 3) / 4 * 4);
     if (e != hipSuccess) return e;
-    return qmr::launch_affine_mfma(a, pl, reinterpret_cast<float *>(fixed), counters, dev->stream);
+    wait.reset_slots = true;
+    e = qmr::launch_affine_mfma(a, pl, reinterpret_cast<unsigned long long *>(fixed), counters, 1u, wait,
+                                dev->stream);
+    if (e != hipSuccess) mark_static_dirty(dev, extent);
+    return e;
 }
 
 // One packed-affine product of at most four RHS: the row-band matrix-core
@@ -558,7 +596,7 @@ int qmr_device_open(int ordinal, const qmr_device_options *options, qmr_device *
         try {
             const ScratchEntry se = scratch_entry(ordinal);
             dev->scratch = se.address;
-            dev->scratch_clean = se.clean;
+            dev->scratch_dirty = se.dirty;
             void *st = nullptr;
             check_hip(hipHostMalloc(&st, 64, hipHostMallocMapped | hipHostMallocCoherent), "hipHostMalloc (status)");
             dev->status_host = static_cast<uint32_t *>(st);
@@ -584,7 +622,6 @@ void qmr_device_close(qmr_device *device) {
         hipStreamSynchronize(device->stream);
         hipStreamDestroy(device->stream);
     }
-    if (device->ws_partial) hipFree(device->ws_partial);
     if (device->ws_wide) hipFree(device->ws_wide);
     if (device->ws_slots) hipFree(device->ws_slots);
     if (device->ws_counters) hipFree(device->ws_counters);
@@ -827,20 +864,26 @@ int qmr_command_finish(qmr_command *command, qmr_frame_timing *timing) {
         command->finished = true;
         if (e == hipSuccess) e = hipGetLastError();
         check_hip(e, "GPU command failed");
-        // A row-band launch of this command whose last split gave up waiting
-        // for its band's other splits (they were not all resident at once)
-        // wrote NaN for that band: the command failed, as a Metal command
-        // buffer whose status is not Completed does (src/gpu.rs:861-865).
-        // The static scratch may then hold sums that no launch cleared.
+        // A launch of this command whose last K split gave up waiting for
+        // the other splits' sums (row-band kernel: its band's workgroups were
+        // not all resident at once; split-K kernel: a tagged slot never
+        // arrived) wrote NaN for that band: the command failed, as a Metal
+        // command buffer whose status is not Completed does
+        // (src/gpu.rs:861-865). The static scratch may then hold sums that no
+        // launch cleared.
         qmr_device *dev = command->device;
         const uint32_t status = __atomic_load_n(dev->status_host, __ATOMIC_ACQUIRE);
         if (status != 0) {
             __atomic_store_n(dev->status_host, 0u, __ATOMIC_RELEASE);
-            dev->scratch_clean->store(false);
+            mark_static_dirty(dev, QMR_STATIC_SCRATCH_BYTES);
+            const bool split_k = (status & 0x40000000u) != 0;
             throw Error{QMR_ERR_DEVICE,
-                        "GPU command failed: affine_band_kernel band " + std::to_string(status & 0x7FFFFFFFu) +
-                            ": the last K split gave up waiting for the other splits' sums (the band's "
-                            "workgroups were not all resident at once); the command's outputs are not valid"};
+                        std::string("GPU command failed: ") + (split_k ? "affine_mfma_kernel" : "affine_band_kernel") +
+                            " band " + std::to_string(status & 0x3FFFFFFFu) +
+                            (split_k ? ": the last K split gave up waiting for the other splits' tagged sums"
+                                     : ": the last K split gave up waiting for the other splits' sums (the band's "
+                                       "workgroups were not all resident at once)") +
+                            "; the command's outputs are not valid"};
         }
         float ms = 0.f;
         check_hip(hipEventElapsedTime(&ms, command->marks[0], end), "hipEventElapsedTime");
@@ -1084,7 +1127,7 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
                 unsigned char *images = fixed;
                 if (fixed) {
                     check_static_scratch(need, "wide-block activation images");
-                    dev->scratch_clean->store(false);
+                    mark_static_dirty(dev, need);
                 }
                 if (!fixed && need > dev->ws_wide_bytes) {
                     check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
@@ -1308,7 +1351,7 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
 
 size_t qmr_device_workspace_bytes(const qmr_device *device) {
     if (!device) return 0;
-    return device->ws_slots_bytes + device->ws_partial_bytes + device->ws_counter_count * sizeof(uint32_t) +
+    return device->ws_slots_bytes + device->ws_counter_count * sizeof(uint32_t) +
            device->ws_wide_bytes;
 }
 

@@ -467,12 +467,9 @@ template <int META, int NRT>
 hipError_t launch_nrt(WideParams p, hipStream_t stream) {
     auto kernel = wide_mfma_kernel<META, NRT>;
     constexpr size_t lds = wide_lds_bytes<META>(NRT);
-    static bool configured = false;
-    if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    {
+        const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kernel), lds);
         if (e != hipSuccess) return e;
-        configured = true;
     }
     p.nrb = (p.rows + 16 * NRT - 1) / (16 * NRT);
     const uint32_t grid = (p.nrb + 7) / 8 * 8 * p.ntb;  // XCD-aware order; surplus workgroups exit

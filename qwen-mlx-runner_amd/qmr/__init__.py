@@ -396,8 +396,8 @@ class Gpu:
         _check(lib().qmr_set_gemv_plan(self._h, rr, ks))
 
     def set_band_wait_fault(self, enabled: bool) -> None:
-        """Testing hook: the row-band kernel's last splits give up (their
-        command's finish then fails)."""
+        """Testing hook: the row-band and split-K kernels' last splits give
+        up (their command's finish then fails)."""
         _check(lib().qmr_set_band_wait_fault(self._h, int(enabled)))
 
     def set_read_plan(self, workgroups: int = 0, unroll: int = 0, nontemporal: int = -1) -> None:

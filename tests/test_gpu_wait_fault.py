@@ -1,13 +1,15 @@
-"""A row-band launch whose last K split gives up must fail its command.
+"""A launch whose last K split gives up waiting must fail its command.
 
-The band kernel's last split waits (boundedly) for the other splits' sums;
-if a band's workgroups were not all resident at once it gives up, writes NaN
-for the band and sets the device's status word, and qmr_command_finish
-returns QMR_ERR_DEVICE naming the band, as the reference fails a frame whose
-Metal command buffer did not complete (src/gpu.rs:861-865).
+The row-band kernel's last split waits (boundedly) for the other splits'
+sums; if a band's workgroups were not all resident at once it gives up,
+writes NaN for the band and sets the device's status word, and
+qmr_command_finish returns QMR_ERR_DEVICE naming the kernel and band, as the
+reference fails a frame whose Metal command buffer did not complete
+(src/gpu.rs:861-865). The split-K kernel's last arriver waits the same way
+for each partial's epoch tag and reports the same way.
 
 The give-up is forced from the host (qmr_set_band_wait_fault: the last
-splits wait for a tag that no split of the launch publishes, with a short
+arrivers wait for a tag that no split of the launch publishes, with a short
 bound), so every workgroup still exits normally. After the failed command the
 same device runs the next command correctly, through qmr_encode and through
 qmr_encode_static, whose scratch the failure leaves to be cleared again.
@@ -50,12 +52,14 @@ def _command(gpu, name, bufs, params, static):
 
 
 @pytest.mark.parametrize("static", [False, True])
-@pytest.mark.parametrize("rows,cols,batch,form,plan", [
-    (5120, 17408, 1, "plain", (0, 0)),      # the metric shape's default plan: three K splits
-    (5120, 17408, 3, "plain", (0, 0)),
-    (4096, 2048, 3, "mlp", (-4, 220202)),   # the MLP form with two K splits
+@pytest.mark.parametrize("rows,cols,batch,form,plan,kernel", [
+    (5120, 17408, 1, "plain", (0, 0), "affine_band_kernel"),      # the metric shape's default plan: three K splits
+    (5120, 17408, 3, "plain", (0, 0), "affine_band_kernel"),
+    (4096, 2048, 3, "mlp", (-4, 220202), "affine_band_kernel"),   # the MLP form with two K splits
+    (5120, 17408, 3, "plain", (-2, 4), "affine_mfma_kernel"),     # split-K, four K splits
+    (4096, 2048, 3, "mlp", (-2, 0), "affine_mfma_kernel"),        # split-K's MLP form
 ])
-def test_give_up_fails_the_command_and_the_next_one_succeeds(gpu, static, rows, cols, batch, form, plan):
+def test_give_up_fails_the_command_and_the_next_one_succeeds(gpu, static, rows, cols, batch, form, plan, kernel):
     rng = np.random.default_rng([rows, cols, batch, int(static)])
     name, arrays, params, want = _inputs(rng, rows, cols, batch, form)
     bufs = [gpu.upload_bytes(np.ascontiguousarray(a)) for a in arrays]
@@ -70,8 +74,8 @@ def test_give_up_fails_the_command_and_the_next_one_succeeds(gpu, static, rows, 
         finally:
             gpu.set_band_wait_fault(False)
         assert err.value.code == qmr.QMR_ERR_DEVICE, err.value
-        assert "affine_band_kernel band" in str(err.value), str(err.value)
-        assert gpu.last_hip_kernel().startswith("affine_band_kernel"), gpu.last_hip_kernel()
+        assert f"{kernel} band" in str(err.value), str(err.value)
+        assert gpu.last_hip_kernel().startswith(kernel), gpu.last_hip_kernel()
         assert " ns=1 " not in gpu.last_hip_kernel(), gpu.last_hip_kernel()
         assert np.isnan(gpu.read_f32(y, batch * rows)).any()
         # The next command on the same device: correct, and its finish succeeds.

@@ -118,16 +118,26 @@ def test_static_entry_matches_qmr_encode_on_two_calls_in_a_row(gpu, form, plan, 
 
 
 def test_static_band_slots_stay_clear_across_a_sequence_of_calls(gpu):
-    """GEMVs and blocks on the row-band kernel clear the split-sum slots they
-    take, so consecutive static calls skip the fill; other paths (the MLP
-    form, split-K) leave the scratch to be cleared again. Every call of a
+    """GEMVs and blocks on the row-band kernel and every split-K launch clear
+    the split-sum slots (and counters) they take, so consecutive static calls
+    skip the fill; the row-band MLP form leaves its slots to be cleared
+    again, over their whole extent: a GEMV that needs fewer slots than the
+    MLP form left behind, followed by a block that needs more, must not find
+    the MLP form's sums in the part the GEMV did not clear. Every call of a
     mixed sequence must match qmr_encode bit for bit."""
     rng = np.random.default_rng(23)
     seq = [("plain", (0, 0), (5120, 17408, 1)), ("plain", (0, 0), (5120, 17408, 3)),
            ("residual", (0, 0), (2048, 8192, 2)), ("plain", (-4, 240202), (4096, 8192, 1)),
            ("mlp", (0, 0), (1024, 2048, 2)), ("plain", (0, 0), (5120, 17408, 2)),
            ("plain", (-2, 0), (4096, 2048, 1)), ("plain", (0, 0), (5120, 17408, 1)),
-           ("plain", (0, 0), (5120, 17408, 1))]
+           ("plain", (0, 0), (5120, 17408, 1)),
+           # MLP slots (2 splits x 2 matrices x 3 RHS x 4096 rows x 8 bytes)
+           # beyond a GEMV's (3 x 5120 x 8) but not a 3-RHS block's.
+           ("mlp", (-4, 220202), (4096, 2048, 3)), ("plain", (0, 0), (5120, 17408, 1)),
+           ("plain", (0, 0), (5120, 17408, 3)),
+           # Split-K's MLP form and a forced four-way split, then the band.
+           ("mlp", (-2, 0), (4096, 2048, 3)), ("plain", (-2, 4), (5120, 17408, 3)),
+           ("plain", (0, 0), (5120, 17408, 3))]
     fresh = qmr.Gpu("aligned")
     try:
         for form, plan, (rows, cols, batch) in seq:
