@@ -83,7 +83,9 @@ struct BandParams {
     uint32_t wait_epoch;  // tag the last split waits for (the epoch; another value forces the give-up, for tests)
     uint32_t spin_limit;
     uint32_t *status;     // set to 0x80000000 | band by a last split that gives up (may be null)
-    uint32_t reset_slots; // nonzero: the last split clears each slot it took (plain and residual forms)
+    uint32_t reset_slots; // nonzero: the finisher clears each slot it took (plain and residual forms)
+    uint32_t elect;       // nonzero: every split publishes and an arrival counter elects the finisher
+    uint32_t *counters;   // [nbands] arrival counters when elected (zero between launches)
     uint32_t rows, cols;
     uint32_t w_bytes, m_bytes;  // extents of the code and metadata views
     uint32_t tr, kw, ns, nbands;
@@ -495,21 +497,30 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     // One thread per output row and RHS (the MLP form: per gate row, whose
     // up row is H tiles further down the band).
     const uint32_t outs = H * 16u * B;
-    if (uint32_t(tid) >= outs) return;
     const uint32_t tt = uint32_t(tid) / (16u * B);  // tile within the band (of the gate rows)
     const uint32_t t = (uint32_t(tid) / 16u) % B;
     const uint32_t rr = uint32_t(tid) % 16u;
     const uint32_t row = band_row0 + tt * 16u + rr;
-    if (row >= p.rows) return;
+    const bool live = uint32_t(tid) < outs && row < p.rows;
+    // Elected finishers (plans over several rounds of workgroups): every
+    // split publishes, and the band's last workgroup to arrive (an arrival
+    // counter elects it) finishes, so no workgroup waits for one that is not
+    // resident. Otherwise the band's last split finishes and the others only
+    // publish. Threads without an output row leave here unless the election
+    // needs them at its barriers.
+    const bool elect = p.elect != 0 && p.ns > 1;
+    if (!live && !elect) return;
     auto wave_sum_of = [&](uint32_t tile) -> float {
         const float *src = red + (size_t(tile * KW) * B + t) * 16u + rr;
         float sum = src[0];
         for (uint32_t k = 1; k < KW; ++k) sum += src[size_t(k) * B * 16u];
         return sum;
     };
-    float v = wave_sum_of(tt);
+    const float v = live ? wave_sum_of(tt) : 0.f;
     const size_t oy = size_t(t) * p.rows + row;
     const size_t stride = size_t(B) * p.rows;
+    // Slot sets: one per publishing split (all ns when elected, else ns-1).
+    const uint32_t nsets = elect ? p.ns : p.ns - 1;
     // Reads slot set k's value for oy once its epoch is this launch's;
     // past the host's spin limit it gives up: the caller writes NaN and
     // reports the band in the status word, which the host turns into a
@@ -535,36 +546,60 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         __hip_atomic_store(q, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     auto publish = [&](uint32_t k, float value) { publish_at(p.partial + size_t(k) * stride + oy, value); };
+    // The election, after this workgroup's slots are published (every
+    // thread calls it): whether this workgroup finishes the band. The counter
+    // only elects; a finisher takes each slot once it carries the launch's
+    // epoch, so no ordering between the slot stores and the increments is
+    // needed. The finisher returns the counter to zero (every other split of
+    // the band has incremented it by then).
+    auto elected = [&]() -> bool {
+        __syncthreads();  // every wave is past its reads of red and sq
+        int *flag = reinterpret_cast<int *>(red);
+        if (tid == 0) {
+            const uint32_t prev = __hip_atomic_fetch_add(&p.counters[band], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = prev + 1 == p.ns;
+            if (last) __hip_atomic_store(&p.counters[band], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = last ? 1 : 0;
+        }
+        __syncthreads();
+        return *flag != 0;
+    };
     if constexpr (MLP) {
-        // Slot sets [2*split] (gate) and [2*split + 1] (up) for splits
-        // 0..ns-2, then their sums of squares [split][band][B]; the band's
-        // last split adds each in split order.
-        const float vu = wave_sum_of(tt + H);
+        // Slot sets [2*k] (gate) and [2*k + 1] (up) of publishing split k,
+        // then their sums of squares [k][band][B]; the finisher adds each in
+        // split order, its own sums in its split's place.
+        const float vu = live ? wave_sum_of(tt + H) : 0.f;
         float ss = 0.f;
         for (uint32_t wv = 0; wv < p.tr * KW; ++wv) ss += sq[wv * B + t];
         // Split k's sum of squares for this band and RHS (ns > 1 only).
         auto sq_slot = [&](uint32_t k) {
-            return p.partial + size_t(2) * (p.ns - 1) * stride + (size_t(k) * p.nbands + band) * B + t;
+            return p.partial + size_t(2) * nsets * stride + (size_t(k) * p.nbands + band) * B + t;
         };
-        if (!finisher) {
+        auto publish_all = [&]() {
             publish(2 * split, v);
             publish(2 * split + 1, vu);
             if (tt == 0 && rr == 0) publish_at(sq_slot(split), ss);
+        };
+        if (elect) {
+            if (live) publish_all();
+            if (!elected() || !live) return;
+        } else if (!finisher) {
+            publish_all();
             return;
         }
         bool ok = true;
         float g = v, u = vu;
         if (p.ns > 1) {
-            float sg = take(0, ok), su = take(1, ok);
-            for (uint32_t k = 1; k + 1 < p.ns; ++k) {
-                sg += take(2 * k, ok);
-                su += take(2 * k + 1, ok);
+            float sg = split == 0 ? v : take(0, ok), su = split == 0 ? vu : take(1, ok);
+            float sx = split == 0 ? ss : take_at(sq_slot(0), ok);
+            for (uint32_t k = 1; k < p.ns; ++k) {
+                sg += k == split ? v : take(2 * k, ok);
+                su += k == split ? vu : take(2 * k + 1, ok);
+                sx += k == split ? ss : take_at(sq_slot(k), ok);
             }
-            g = sg + v;
-            u = su + vu;
-            float sx = take_at(sq_slot(0), ok);
-            for (uint32_t k = 1; k + 1 < p.ns; ++k) sx += take_at(sq_slot(k), ok);
-            ss = sx + ss;
+            g = sg;
+            u = su;
+            ss = sx;
         }
         const float inv = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
         const float gn = g * inv;
@@ -572,26 +607,31 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         report(ok);
         return;
     } else {
+        float y = v;
         if (p.ns > 1) {
-            if (split + 1 < p.ns) {
+            if (elect) {
+                if (live) publish(split, v);
+                if (!elected() || !live) return;
+            } else if (split + 1 < p.ns) {
                 publish(split, v);
                 return;
             }
-            // The band's last split: the other splits' sums, in split order.
-            // Each slot is this thread's alone, so with reset_slots it is
-            // cleared once taken, leaving the workspace zero for the next
-            // launch (which may then reuse the same epoch).
+            // The finisher: every split's sum in split order, its own in its
+            // place. Each slot is this thread's alone, so with reset_slots it
+            // is cleared once taken (the finisher's own too when it was
+            // published), leaving the workspace zero for the next launch
+            // (which may then reuse the same epoch).
             bool ok = true;
-            float sum = take(0, ok);
-            for (uint32_t k = 1; k + 1 < p.ns; ++k) sum += take(k, ok);
+            float sum = split == 0 ? v : take(0, ok);
+            for (uint32_t k = 1; k < p.ns; ++k) sum += k == split ? v : take(k, ok);
             if (p.reset_slots)
-                for (uint32_t k = 0; k + 1 < p.ns; ++k)
+                for (uint32_t k = 0; k < nsets; ++k)
                     __hip_atomic_store(p.partial + size_t(k) * stride + oy, 0ull, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
-            v = ok ? sum + v : __builtin_nanf("");
+            y = ok ? sum : __builtin_nanf("");
             report(ok);
         }
-        p.y[oy] = FUSE == 1 ? p.r[oy] + v : v;
+        p.y[oy] = FUSE == 1 ? p.r[oy] + y : y;
     }
 }
 
@@ -852,12 +892,14 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     // rounds measured slower at both batches.
     double best = 1e30;
     for (int pass = 0; pass < 2 && pl.kw == 0; ++pass) {
-        if (pass == 1 && (mlp || (force_ns && force_ns != 1))) break;
+        // Several rounds: single-split bands; split bands with elected
+        // finishers (no workgroup waits) and the MLP form only when forced.
+        if (pass == 1 && mlp && !force_ns) break;
         for (uint32_t ring : {2u, 3u}) {
             if (force_ring && ring != force_ring) continue;
             for (uint32_t ns = 1; ns <= 4; ++ns) {
                 if (force_ns && ns != force_ns) continue;
-                if (pass == 1 && ns != 1) continue;
+                if (pass == 1 && ns != 1 && !force_ns) continue;
                 if (ns > n_entries) continue;
                 uint32_t max_se = 0;
                 bool empty = false;
@@ -922,6 +964,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                             pl.xi = xi;
                             pl.ring = ring;
                             pl.lds = lds;
+                            pl.elect = pass == 1 && ns > 1;
                         }
                     }
                 }
@@ -944,15 +987,17 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
 
 size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a) {
     if (pl.ns <= 1) return 0;
+    const size_t sets = pl.elect ? pl.ns : pl.ns - 1;  // publishing splits
     if (a.up_w)  // gate and up sums per row, then each band's sums of x^2
-        return size_t(pl.ns - 1) * (size_t(2) * a.rows + pl.nbands) * a.batch * sizeof(unsigned long long);
-    return size_t(pl.ns - 1) * a.batch * a.rows * sizeof(unsigned long long);
+        return sets * (size_t(2) * a.rows + pl.nbands) * a.batch * sizeof(unsigned long long);
+    return sets * a.batch * a.rows * sizeof(unsigned long long);
 }
 
-hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial, uint32_t epoch,
-                              const TileWait &wait, hipStream_t stream) {
+hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial, uint32_t *counters,
+                              uint32_t epoch, const TileWait &wait, hipStream_t stream) {
     if (pl.kw == 0) return hipErrorInvalidValue;
     if (pl.ns > 1 && partial == nullptr) return hipErrorInvalidValue;
+    if (pl.elect && pl.ns > 1 && counters == nullptr) return hipErrorInvalidValue;
     BandParams p;
     p.w = a.w;
     p.s = a.s;
@@ -973,6 +1018,8 @@ hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned 
     p.spin_limit = wait.force_give_up ? 64u : 1u << 22;
     p.status = wait.status;
     p.reset_slots = wait.reset_slots && a.up_w == nullptr ? 1u : 0u;
+    p.elect = pl.elect && pl.ns > 1 ? 1u : 0u;
+    p.counters = counters;
     p.rows = a.rows;
     p.cols = a.cols;
     p.w_bytes = uint32_t(uint64_t(a.rows) * a.cols * a.bits / 8);

@@ -168,6 +168,7 @@ struct TilePlan {
     uint32_t xi = 0;          // x items staged per thread
     uint32_t ring = 0;        // code entries in flight per wave (2 or 3)
     size_t lds = 0;           // dynamic LDS bytes per workgroup
+    bool elect = false;       // every split publishes; an arrival counter elects each band's finisher
 };
 bool affine_tile_supported(const AffineArgs &a);
 // Zeros leave the choice to the planner.
@@ -178,8 +179,10 @@ size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a);
 // `partial` holds affine_tile_workspace bytes (64-bit slots: a slot counts
 // only when its epoch matches); `epoch` must differ from the previous
 // launch's that used the same slots, unless those slots were cleared.
+// `counters` holds pl.nbands zeroed u32 when pl.elect (the kernel returns
+// them to zero); otherwise it may be null.
 hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned long long *partial,
-                              uint32_t epoch, const TileWait &wait, hipStream_t stream);
+                              uint32_t *counters, uint32_t epoch, const TileWait &wait, hipStream_t stream);
 
 // Wide block on MFMA (Q4/g64, F32 or BF16 metadata, batch up to 256): a prep
 // launch converts x into per-group images in `workspace` (wide_mfma_workspace

@@ -432,37 +432,45 @@ qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a,
     return pl;
 }
 
-// Launch the row-band kernel over the device's slot workspace, or with
-// `fixed` (qmr_encode_static) over the static scratch.
+// Launch the row-band kernel over the device's slot workspace (and, for
+// plans with elected finishers, its arrival counters), or with `fixed`
+// (qmr_encode_static) over the static scratch: slots, then counters.
 hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::TilePlan &pl,
                        unsigned char *fixed) {
     const size_t need = qmr::affine_tile_workspace(pl, a);
+    const bool elect = pl.elect && pl.ns > 1;
     dev->last_hip = "affine_band_kernel ring=" + std::to_string(pl.ring) + " ns=" + std::to_string(pl.ns) +
-                    " tr=" + std::to_string(pl.tr) + " kw=" + std::to_string(pl.kw);
+                    " tr=" + std::to_string(pl.tr) + " kw=" + std::to_string(pl.kw) + (elect ? " elect" : "");
     qmr::TileWait wait;
     wait.status = dev->status_dev;
     wait.force_give_up = dev->force_give_up;
     if (fixed) {
         // The sums are tagged with epoch 1, which no cleared slot carries.
-        // The plain and residual forms' last splits clear each slot they
-        // take, so once the slot region is zero it stays zero from launch to
-        // launch and needs no fill; it is cleared when earlier launches may
-        // have left it non-zero: first use on this GPU, after the split-K or
-        // wide paths used the scratch, after an MLP form (whose slots are
+        // The plain and residual forms' finishers clear each slot (and
+        // counter) they take, so once the region is zero it stays zero from
+        // launch to launch and needs no fill; it is cleared when earlier
+        // launches may have left it non-zero: first use on this GPU, after
+        // the wide path used the scratch, after an MLP form (whose slots are
         // not cleared) and after a command that failed.
-        check_static_scratch(need, "row-band split sums");
+        const size_t part = (need + 255) / 256 * 256;
+        const size_t extent = elect ? part + size_t(pl.nbands) * sizeof(uint32_t) : need;
+        check_static_scratch(extent, "row-band split sums");
         start_gpu(dev);
         const bool plain = a.up_w == nullptr;
-        hipError_t e = clear_static_slots(dev, fixed, need);
+        hipError_t e = clear_static_slots(dev, fixed, (extent + 3) / 4 * 4);
         if (e != hipSuccess) return e;
         wait.reset_slots = plain;
-        e = qmr::launch_affine_tile(a, pl, reinterpret_cast<unsigned long long *>(fixed), 1u, wait, dev->stream);
-        if (!plain || e != hipSuccess) mark_static_dirty(dev, need);
+        uint32_t *counters = elect ? reinterpret_cast<uint32_t *>(fixed + part) : nullptr;
+        e = qmr::launch_affine_tile(a, pl, reinterpret_cast<unsigned long long *>(fixed), counters, 1u, wait,
+                                    dev->stream);
+        if (!plain || e != hipSuccess) mark_static_dirty(dev, extent);
         return e;
     }
     const uint32_t epoch = next_slot_epoch(dev, need);
+    if (elect) ensure_counters(dev, pl.nbands);
     start_gpu(dev);
-    return qmr::launch_affine_tile(a, pl, dev->ws_slots, epoch, wait, dev->stream);
+    return qmr::launch_affine_tile(a, pl, dev->ws_slots, elect ? dev->ws_counters : nullptr, epoch, wait,
+                                   dev->stream);
 }
 
 // Launch the split-K kernel with its partial-sum slots and per-band arrival

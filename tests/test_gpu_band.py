@@ -183,3 +183,46 @@ def test_band_residual_form(gpu, in_place, ring, ns, tr, kw):
     got = gpu.read_f32(yb, batch * rows)
     want = oracle.matmul_f64(*m, "bf16", x, rows, cols, 4, 64, batch, 16) + r.astype(np.float64)
     assert_gate(got, want, f"residual in_place={in_place}")
+
+
+@pytest.mark.parametrize("rows,cols,batch,bits,kind,plan", [
+    (40960, 2048, 2, 4, "bf16", (2, 4, 8, 1)),   # 1280 workgroups of 8 waves: several rounds
+    (70000, 1152, 3, 8, "f32", (3, 2, 8, 1)),    # Q8 FP32, a row tail
+    (24576, 4096, 1, 4, "f16", (2, 3, 4, 2)),
+])
+def test_elected_finishers_over_several_rounds(gpu, rows, cols, batch, bits, kind, plan):
+    """Forced split plans whose workgroups do not fit one round (more than
+    four 8-wave workgroups per CU) run with elected finishers: every split
+    publishes its sums and the band's last workgroup to arrive (an arrival
+    counter) adds them in split order, so no workgroup waits for one that is
+    not resident. Against the FP64 oracle, and deterministic."""
+    rng = np.random.default_rng([rows, cols, batch])
+    m = _matrix(rng, rows, cols, bits, 64, kind)
+    x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
+    want = oracle.matmul_f64(*m, kind, x, rows, cols, bits, 64, batch, 16)
+    print(f"elected finishers {rows}x{cols} Q{bits} {kind} B={batch} plan {plan}", flush=True)
+    got, kernel = _run(gpu, m, x, rows, cols, bits, 64, batch, kind, (-4, _ks(*plan)))
+    ring, ns, tr, kw = plan
+    assert kernel == f"affine_band_kernel ring={ring} ns={ns} tr={tr} kw={kw} elect", kernel
+    assert_gate(got, want, f"elected {rows}x{cols} plan {plan}")
+    again, _ = _run(gpu, m, x, rows, cols, bits, 64, batch, kind, (-4, _ks(*plan)))
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "launches differ"
+
+
+def test_elected_finishers_residual_form_in_place(gpu):
+    rng = np.random.default_rng(41)
+    rows, cols, batch, plan = 40960, 2048, 3, (3, 4, 8, 1)
+    m = _matrix(rng, rows, cols, 4, 64, "bf16")
+    x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
+    r = rng.normal(0, 1, batch * rows).astype(np.float32)
+    bufs = [gpu.upload_bytes(np.ascontiguousarray(a)) for a in m] + [gpu.upload_f32(x.ravel())]
+    rb = gpu.upload_f32(r)
+    gpu.set_gemv_plan(-4, _ks(*plan))
+    try:
+        gpu.dispatch("matmul_affine_add_bf16", bufs + [rb, rb], [rows, cols, 4, 64, batch])
+        kernel = gpu.last_hip_kernel()
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    assert kernel.endswith(" elect"), kernel
+    want = oracle.matmul_f64(*m, "bf16", x, rows, cols, 4, 64, batch, 16) + r.astype(np.float64)
+    assert_gate(gpu.read_f32(rb, batch * rows), want, "elected residual in place")

@@ -105,6 +105,33 @@ def test_mlp_band_form_forced_plans(gpu, plan, rows, cols, bits, group, batch, k
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "launches differ"
 
 
+@pytest.mark.parametrize("plan,batch", [(320801, 3), (220401, 2), (340401, 4)])
+def test_mlp_band_form_with_elected_finishers(gpu, plan, batch):
+    """The row-band MLP form at the 27B gate/up shape under forced split
+    plans whose workgroups take several rounds: every split publishes its
+    gate, up and sum-of-squares slots, and the band's last workgroup to
+    arrive finishes. Against the FP64 oracle and deterministic."""
+    rows, cols = 17408, 5120
+    rng = np.random.default_rng(plan + batch)
+    gate_m = _matrix(rng, rows, cols, 4, 64, "bf16")
+    up_m = _matrix(rng, rows, cols, 4, 64, "bf16")
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    want = oracle.mlp_gate_up_f64(gate_m, up_m, "bf16", x, nw, EPS, rows, cols, 4, 64, batch, 16)
+    print(f"mlp elected plan {plan} B={batch}", flush=True)
+    gpu.set_gemv_plan(-4, plan)
+    try:
+        got = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, 4, 64, batch, "bf16")
+        kernel = gpu.last_hip_kernel()
+        again = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, 4, 64, batch, "bf16")
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    ring, ns, tr, kw = plan // 100000, plan // 10000 % 10, plan // 100 % 100, plan % 100
+    assert kernel == f"affine_band_kernel ring={ring} ns={ns} tr={tr} kw={kw} elect (MLP)", kernel
+    assert_gate(got, want, f"mlp elected {plan} B{batch}")
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "launches differ"
+
+
 @pytest.mark.parametrize("batch", [1, 3])
 def test_mlp_default_is_the_band_kernel_at_the_27b_shape(gpu, batch):
     """At the 27B gate/up shape and B=1 the fused form runs on the row-band

@@ -58,6 +58,7 @@ def _command(gpu, name, bufs, params, static):
     (4096, 2048, 3, "mlp", (-4, 220202), "affine_band_kernel"),   # the MLP form with two K splits
     (5120, 17408, 3, "plain", (-2, 4), "affine_mfma_kernel"),     # split-K, four K splits
     (4096, 2048, 3, "mlp", (-2, 0), "affine_mfma_kernel"),        # split-K's MLP form
+    (40960, 2048, 2, "plain", (-4, 240801), "affine_band_kernel"),  # elected finishers, several rounds
 ])
 def test_give_up_fails_the_command_and_the_next_one_succeeds(gpu, static, rows, cols, batch, form, plan, kernel):
     rng = np.random.default_rng([rows, cols, batch, int(static)])

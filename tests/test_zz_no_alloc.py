@@ -137,7 +137,10 @@ def test_static_band_slots_stay_clear_across_a_sequence_of_calls(gpu):
            ("plain", (0, 0), (5120, 17408, 3)),
            # Split-K's MLP form and a forced four-way split, then the band.
            ("mlp", (-2, 0), (4096, 2048, 3)), ("plain", (-2, 4), (5120, 17408, 3)),
-           ("plain", (0, 0), (5120, 17408, 3))]
+           ("plain", (0, 0), (5120, 17408, 3)),
+           # Elected finishers: slots of every split, then the arrival counters.
+           ("plain", (-4, 240801), (40960, 2048, 2)), ("plain", (-4, 240801), (40960, 2048, 2)),
+           ("plain", (0, 0), (5120, 17408, 1))]
     fresh = qmr.Gpu("aligned")
     try:
         for form, plan, (rows, cols, batch) in seq:
