@@ -870,15 +870,20 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     // workgroup must be resident in one round (a second round repeats the
     // start-up latency). Score, fitted to timings on MI355X of every feasible
     // plan of six shapes (5120x17408, 17408x5120 and 12288x4096 Q4,
-    // 17408x5120 Q8, 5120x5120 Q4 and Q8) at B=1 and B=3:
-    //   0.5 |log2(waves / two per SIMD)|
+    // 17408x5120 Q8, 5120x5120 Q4 and Q8) at B=1..4:
+    //   0.25 |log2(waves / two per SIMD)|
     //   + log2(workgroups per CU rounded up / the even share)
-    //   + x bytes read from L2 (once per band) / weight bytes
-    //   + |log2(codes in flight per CU / 36 KB)|, with waves per CU x ring
-    //     x 2 KB entries in flight: the stream is fastest near 36 KB and
-    //     slows with less (latency not covered) and with more (at 5120x17408
-    //     B=1: 12.2 us with 30 KB, 11.9 with 45, 12.3 with 60)
+    //   + 2 x bytes read from L2 (once per band) / weight bytes: every band
+    //     converts its x, which the stream waits for
+    //   + 0.5 |log2(codes in flight per CU / 36 KB)|, with waves per CU x
+    //     ring x 2 KB entries in flight: the stream slows with less (latency
+    //     not covered) and with more (at 5120x17408 B=1: 12.2 us with 30 KB,
+    //     11.9 with 45, 12.3 with 60)
     //   + 0.1 for a two-entry ring.
+    // Against the best measured plan of each of the 24 cases, two sweeps on
+    // two runs: the previous weights (0.5, 1, 1, 1) lost 9.9 and 10.4 us in
+    // total, these 4.9 and 4.8 (17408x5120 Q4 at B=2..4 takes three splits
+    // of 8-tile bands: 15.9-17.0 -> 15.1-15.4 us).
     // Where no plan fits one round (a 151936-row vocabulary head), a second
     // pass takes single-split bands, whose workgroups never wait on each
     // other, so any number of rounds is safe: the tallest band, one wave per
@@ -941,10 +946,10 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                             if (wgs > double(resident) * cus) continue;
                             const double waves = wgs * tr * kw;
                             const double per_cu = std::ceil(wgs / cus) / (wgs / cus);
-                            score = 0.5 * std::fabs(std::log2(waves / (2.0 * 4 * cus)));
+                            score = 0.25 * std::fabs(std::log2(waves / (2.0 * 4 * cus)));
                             score += std::log2(per_cu);
-                            score += double(nbands) * a.batch * a.cols * 4.0 / (wbytes * (mlp ? 2 : 1));
-                            score += std::fabs(std::log2(waves / cus * ring * 2048.0 / 36864.0));
+                            score += 2.0 * double(nbands) * a.batch * a.cols * 4.0 / (wbytes * (mlp ? 2 : 1));
+                            score += 0.5 * std::fabs(std::log2(waves / cus * ring * 2048.0 / 36864.0));
                             score += ring == 2 ? 0.1 : 0.0;
                         } else {
                             const double flight = double(resident) * tr * kw * ring * 2048.0;
@@ -971,14 +976,16 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
             }
         }
     }
-    // Short streams at one RHS: fewer than 8 entries per wave, where x costs
-    // little to convert, run faster with half the row tiles per band (more,
-    // shorter workgroups). Measured on one box, every feasible plan timed:
-    // 5120x5120 Q8 9.18 -> 8.36 us, Q4 7.74 -> 7.54 us; at B=3 halving cost
-    // 0.57 us on Q4, and the longer streams of the other fitted shapes
-    // (8-20 entries per wave) keep their plans.
-    if (pl.kw > 0 && !mlp && a.batch == 1 && pl.tr >= 4 && !force_kw && !force_tr && !force_ns && !force_ring &&
-        pl.n_entries < 8 * pl.ns * pl.kw) {
+    // Short streams: fewer than 8 entries per wave run faster with half the
+    // row tiles per band (more, shorter workgroups) where x costs little to
+    // convert against the codes: at one RHS, and for 8-bit codes (twice the
+    // bytes per staged column). Measured on one box, every feasible plan
+    // timed: 5120x5120 Q8 9.18 -> 8.36 us, Q4 7.74 -> 7.54 us at B=1; at B=3
+    // Q8 9.37 -> 9.23 and, on another box, 9.62 -> 9.25 us, while halving
+    // cost Q4 0.57 us. The longer streams of the other fitted shapes (8-20
+    // entries per wave) keep their plans.
+    if (pl.kw > 0 && !mlp && (a.batch == 1 || a.bits == 8) && pl.tr >= 4 && !force_kw && !force_tr && !force_ns &&
+        !force_ring && pl.n_entries < 8 * pl.ns * pl.kw) {
         const TilePlan half = plan_affine_tile(a, lim, pl.kw, pl.tr / 2, pl.ns, pl.ring);
         if (half.kw > 0) pl = half;
     }
