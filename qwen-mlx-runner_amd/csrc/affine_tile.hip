@@ -875,15 +875,19 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     //   + log2(workgroups per CU rounded up / the even share)
     //   + 2 x bytes read from L2 (once per band) / weight bytes: every band
     //     converts its x, which the stream waits for
-    //   + 0.5 |log2(codes in flight per CU / 36 KB)|, with waves per CU x
+    //   + 0.25 |log2(codes in flight per CU / 36 KB)|, with waves per CU x
     //     ring x 2 KB entries in flight: the stream slows with less (latency
     //     not covered) and with more (at 5120x17408 B=1: 12.2 us with 30 KB,
     //     11.9 with 45, 12.3 with 60)
-    //   + 0.1 for a two-entry ring.
+    //   + 0.1 for a two-entry ring
+    //   + 4 splits / entries per row: short splits read their rows'
+    //     metadata in short runs.
     // Against the best measured plan of each of the 24 cases, two sweeps on
-    // two runs: the previous weights (0.5, 1, 1, 1) lost 9.9 and 10.4 us in
-    // total, these 4.9 and 4.8 (17408x5120 Q4 at B=2..4 takes three splits
-    // of 8-tile bands: 15.9-17.0 -> 15.1-15.4 us).
+    // two runs: the previous weights (0.5, 1, 1, 1, 0.1, 0) lost 9.9 and
+    // 10.4 us in total, these 3.9 and 3.8 (17408x5120 Q4 at B=2..4 takes
+    // three splits of 8-tile bands: 15.9-17.0 -> 15.0-15.4 us; 12288x4096
+    // at B=1 and B=2 single-split 4-tile bands of two waves: 9.1 -> 8.9,
+    // 10.0 -> 9.1 us).
     // Where no plan fits one round (a 151936-row vocabulary head), a second
     // pass takes single-split bands, whose workgroups never wait on each
     // other, so any number of rounds is safe: the tallest band, one wave per
@@ -949,8 +953,9 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
                             score = 0.25 * std::fabs(std::log2(waves / (2.0 * 4 * cus)));
                             score += std::log2(per_cu);
                             score += 2.0 * double(nbands) * a.batch * a.cols * 4.0 / (wbytes * (mlp ? 2 : 1));
-                            score += 0.5 * std::fabs(std::log2(waves / cus * ring * 2048.0 / 36864.0));
+                            score += 0.25 * std::fabs(std::log2(waves / cus * ring * 2048.0 / 36864.0));
                             score += ring == 2 ? 0.1 : 0.0;
+                            score += 4.0 * ns / n_entries;
                         } else {
                             const double flight = double(resident) * tr * kw * ring * 2048.0;
                             score = double(8 / tr) + double(kw) + std::fabs(std::log2(flight / 49152.0));
