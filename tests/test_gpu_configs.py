@@ -4,8 +4,9 @@ dequantisation of sampled rows:
   1: Q4/g64 BF16 17408x5120 and 5120x17408, B=1
   2: the same matrices, B=3 (MTP verification block)
   3: Q8/g64 5120x5120 with F16 and with FP32 metadata; Q4/g64 BF16 head
-     151936x5120 at B=1 and B=3 (rows sampled for the oracle)
-  4: wide block 17408x5120 x 128 RHS (rows sampled for the oracle)
+     151936x5120 at B=1 and B=3 (every row against the oracle)
+  4: wide block 17408x5120 x 128 and x 256 RHS (every row against the
+     oracle)
 """
 import os
 
@@ -79,9 +80,8 @@ def test_config3_q8_f16_and_f32_metadata(gpu):
 def test_config3_vocabulary_head(gpu):
     rows, cols = synth.HEAD_SHAPE
     m = synth.q4_bf16_matrix(rows, cols, SEED, tag="head")
-    sample = sorted(set(list(range(0, rows, 97)) + [rows - 1]))
-    check(gpu, m, 1, sample)
-    check(gpu, m, 3, sample)
+    check(gpu, m, 1)
+    check(gpu, m, 3)
     check_dequant_rows(gpu, m, [0, rows - 1])
 
 
@@ -105,8 +105,8 @@ def test_multi_round_band_plan_on_a_ragged_tall_matrix(gpu):
 def test_config4_wide_block(gpu, batch):
     rows, cols = synth.MLP_SHAPES["gate_up"]
     m = synth.q4_bf16_matrix(rows, cols, SEED, tag="gate_up")
-    sample = sorted(set(list(range(0, rows, 271)) + [rows - 1]))
-    check(gpu, m, batch, sample, name="matmul_affine_wide_bf16")
+    print(f"config 4: {batch} RHS, every row against the oracle", flush=True)
+    check(gpu, m, batch, name="matmul_affine_wide_bf16")
 
 
 @pytest.mark.parametrize("rows,cols,batch,meta", [(300, 1024, 100, "bf16"), (128, 512, 64, "f32"),
