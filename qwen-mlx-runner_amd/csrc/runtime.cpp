@@ -1081,13 +1081,16 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
                 // 26.1 us at B=1 and 30.4 at B=3 against 29.4 and 35.5 for
                 // the row-owning MLP mode, although both matrices' grid takes
                 // two rounds of resident workgroups), also when the hook asks
-                // for it (rr == -2); the row-owning kernel's MLP mode when
+                // for it (rr == -2, with ks > 0 K splits when feasible); the
+                // row-owning kernel's MLP mode when
                 // the hook asks for it (rr == -3, ks = j*10000 + rt*100 + kw)
                 // or split-K has no plan.
                 const qmr::GemvPlan f = dev->forced_plan;
                 qmr::TilePlan bp;
                 if ((f.rr == 0 || f.rr == -4) && qmr::affine_tile_supported(a)) bp = forced_tile_plan(dev, a);
-                const qmr::MfmaPlan mp = bp.kw > 0 ? qmr::MfmaPlan{} : qmr::plan_affine_mfma(a, dev->limits);
+                const qmr::MfmaPlan mp =
+                    bp.kw > 0 ? qmr::MfmaPlan{}
+                              : qmr::plan_affine_mfma(a, dev->limits, f.rr == -2 && f.ks > 0 ? uint32_t(f.ks) : 0u);
                 if (bp.kw > 0) {
                     e = launch_band(dev, a, bp, fixed);
                     dev->last_hip += " (MLP)";
