@@ -245,13 +245,23 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *            tr*100 + kw pins its ring depth (2 or 3), K splits, row tiles
  *            per band (the MLP form: tr/2 gate and tr/2 up tiles) and waves
  *            per tile; zero fields and ks = 0 leave them to its planner.
+ *   rr = -5: dense F16 products (matvec_f16, matmul_f16) on the matrix-core
+ *            kernel with ks = ring*10000 + kw*1000 + rt*100 + ns (entries
+ *            in flight per wave, 4 or 8; waves per row tile; row tiles per
+ *            workgroup; K splits; zero fields and ks = 0 leave them to its
+ *            planner). Dense
+ *            products run on that kernel by default wherever it supports
+ *            the view (16-byte aligned weights, cols % 32 == 0); rr = -1
+ *            sends them to the vector-ALU kernels.
  * Shapes a forced kernel does not support fall back to the next one; pairs
  * that are not compiled fall back to the planner. */
 int qmr_set_gemv_plan(qmr_device *device, int rr, int ks);
 /* The plan the GEMV launcher uses for a shape with group 64 and BF16
  * metadata (honours a forced plan), in the encoding of qmr_set_gemv_plan;
  * the row-band kernel reports rr = -4 with its ks, the split-K kernel
- * rr = -2 with ks = its K splits. */
+ * rr = -2 with ks = its K splits. bits = 16: the plan of a dense F16
+ * product over an aligned view (rr = -5 with its ks, or rr = -1 for the
+ * vector-ALU kernels). */
 int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32_t bits,
                   uint32_t batch, int *rr, int *ks);
 /* Tuning hook for "read_checksum" (the read floor a product is measured

@@ -40,6 +40,7 @@ SOURCES = [
     ("affine_mfma.hip", ["-x", "hip"]),
     ("affine_rows.hip", ["-x", "hip"]),
     ("affine_tile.hip", ["-x", "hip"]),
+    ("dense_mfma.hip", ["-x", "hip"]),
     ("misc_kernels.hip", ["-x", "hip"]),
     # MFMA accumulators in VGPRs: the wide kernel's FP32 epilogue adds into
     # the same registers its bias MFMAs accumulate into.

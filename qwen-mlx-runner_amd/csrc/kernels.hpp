@@ -1,6 +1,6 @@
 // Launch interface between the host runtime (runtime.cpp) and the HIP
-// kernels (affine_rows.hip, affine_mfma.hip, affine_gemv.hip,
-// misc_kernels.hip, wide_mfma.hip).
+// kernels (affine_rows.hip, affine_mfma.hip, affine_gemv.hip, affine_tile.hip,
+// dense_mfma.hip, misc_kernels.hip, wide_mfma.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -87,16 +87,16 @@ struct ReadPlan {
 hipError_t launch_read_checksum(const void *a, uint32_t na, const void *b, uint32_t nb, const void *c, uint32_t nc,
                                 uint32_t *out, const ReadPlan &plan, hipStream_t stream);
 // A last arriver's wait on the other K splits' {value, epoch} slots (the
-// row-band and split-K kernels).
+// row-band, split-K and dense kernels).
 struct TileWait {
     // Device-visible word that a last arriver which gives up sets to
     // 0x80000000 | band (row-band kernel: its band's workgroups were not all
-    // resident) or 0xC0000000 | band (split-K kernel); null: no report (the
-    // outputs are NaN either way).
+    // resident), 0xC0000000 | band (split-K kernel) or 0xA0000000 | band
+    // (dense kernel); null: no report (the outputs are NaN either way).
     uint32_t *status = nullptr;
     // The last arriver clears each slot it took (row-band: plain and residual
-    // forms; split-K: every form), so that a workspace that was zero stays
-    // zero and the next launch may reuse the same epoch.
+    // forms; split-K and dense: every form), so that a workspace that was
+    // zero stays zero and the next launch may reuse the same epoch.
     bool reset_slots = false;
     // Testing: the last arriver waits for a tag no split publishes and gives
     // up after a short bound; every workgroup still exits.
@@ -126,6 +126,42 @@ size_t affine_mfma_workspace(const MfmaPlan &pl, const AffineArgs &a);
 // `counters` holds pl.nbands zeroed u32 (the kernel returns them to zero).
 hipError_t launch_affine_mfma(const AffineArgs &a, const MfmaPlan &pl, unsigned long long *slots,
                               uint32_t *counters, uint32_t epoch, const TileWait &wait, hipStream_t stream);
+
+// Dense F16 matvec / block (batch 1..4) on the matrix cores: row bands of
+// 16-row tiles, K in ns splits whose epoch-tagged sums an elected finisher
+// adds. See dense_mfma.hip.
+struct DensePlan {
+    uint32_t rt = 0;      // 16-row tiles per workgroup; 0 = unsupported
+    uint32_t kw = 0;      // waves per tile (contiguous K runs of the split)
+    uint32_t ring = 0;    // 128-byte entries in flight per wave (4 or 8)
+    uint32_t nbands = 0;  // row bands
+    uint32_t ns = 0;      // K splits across workgroups
+    uint32_t tiles = 0;   // 128-column K tiles
+    uint32_t tps = 0;     // K tiles per split
+    uint32_t xi = 0;      // x items staged per thread
+    size_t lds = 0;       // dynamic LDS bytes per workgroup
+    double cost_us = 0;   // the planner's time estimate
+};
+// Fields the tuning hook pins (0 = the planner's choice).
+struct DenseForce {
+    uint32_t ring = 0, kw = 0, rt = 0, ns = 0;
+};
+// 16-byte aligned weights, cols % 32 == 0, 1..4 RHS, views below 2 GiB.
+bool dense_mfma_supported(const uint16_t *w, uint32_t rows, uint32_t cols, uint32_t batch);
+// Pinned fields that no feasible plan has fall back to the planner's plan.
+// The planner scores every feasible plan with a cost model fitted to MI355X
+// timings and keeps the cheapest.
+DensePlan plan_dense_mfma(uint32_t rows, uint32_t cols, uint32_t batch, const DeviceLimits &lim,
+                          const DenseForce &force = DenseForce{});
+size_t dense_mfma_workspace(const DensePlan &pl, uint32_t rows, uint32_t batch);
+// Estimated time (us) of the vector-ALU dense kernels on the same product,
+// for the choice between the two.
+double dense_valu_cost(uint32_t rows, uint32_t cols, uint32_t batch);
+// `slots` (dense_mfma_workspace bytes) and `counters` (pl.nbands zeroed u32)
+// as for launch_affine_mfma; both may be null when pl.ns == 1.
+hipError_t launch_dense_mfma(const uint16_t *w, const float *x, float *y, uint32_t rows, uint32_t cols,
+                             uint32_t batch, const DensePlan &pl, unsigned long long *slots, uint32_t *counters,
+                             uint32_t epoch, const TileWait &wait, hipStream_t stream);
 
 // Streaming GEMV / small block on the matrix cores with every workgroup
 // owning whole rows (no cross-workgroup reduction). See affine_rows.hip.

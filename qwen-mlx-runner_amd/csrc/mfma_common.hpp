@@ -55,12 +55,16 @@ __device__ __forceinline__ float meta_f32(uint32_t v) {
 //   Q4 word -> halves [q0, q4 | q1, q5 | q2, q6 | q3, q7] * 2^-20
 //   Q8 words w0,w1 -> [b0, b2 | b1, b3 | b4, b6 | b5, b7] * 2^-22
 // k_of(e) is the column (within the 8-column chunk) of half e.
+// BITS = 16: dense F16 weights, used as stored (no scale exponent, halves in
+// column order).
 template <int BITS>
-constexpr int kCodeExp = BITS == 4 ? 20 : 22;
+constexpr int kCodeExp = BITS == 4 ? 20 : BITS == 8 ? 22 : 0;
 
 template <int BITS>
 __device__ __forceinline__ int k_of(int e) {
-    if constexpr (BITS == 4) {
+    if constexpr (BITS == 16) {
+        return e;
+    } else if constexpr (BITS == 4) {
         constexpr int k[8] = {0, 4, 1, 5, 2, 6, 3, 7};
         return k[e];
     } else {

@@ -300,6 +300,16 @@ hipError_t launch_dense_f16(const uint16_t *w, const float *x, float *y, uint32_
     return hipGetLastError();
 }
 
+// The streaming kernel's time (us) as the read floor's fixed part plus the
+// weight stream at the measured read rate, stretched per RHS count by the
+// factor measured on MI355X over 2048x5120, 5120x5120, 5120x17408 and
+// 17408x5120 (1.0-1.18 at one RHS, 1.34-1.48 at two, 1.64-1.84 at three,
+// 1.67-2.36 at four; the middle of each range here).
+double dense_valu_cost(uint32_t rows, uint32_t cols, uint32_t batch) {
+    static constexpr double stretch[5] = {1.0, 1.1, 1.4, 1.72, 1.9};
+    return 2.19 + double(rows) * cols * 2.0 / 6.98e6 * stretch[batch < 1 ? 1 : batch > 4 ? 4 : batch];
+}
+
 hipError_t launch_embed_f16(const uint16_t *w, uint32_t row, uint32_t cols, float *y,
                             hipStream_t stream) {
     hipLaunchKernelGGL(embed_f16_kernel, dim3((cols + 255) / 256), dim3(256), 0, stream, w, row,

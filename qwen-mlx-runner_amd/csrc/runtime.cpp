@@ -68,6 +68,9 @@ struct qmr_device {
     // planning enumerates ~100 shapes with occupancy queries, which must not
     // sit on every launch.
     mutable std::map<BandPlanKey, qmr::TilePlan> band_plans;
+    // Dense matrix-core plans by rows, cols, batch and forced plan (-1: the
+    // default choice).
+    mutable std::map<std::tuple<uint32_t, uint32_t, uint32_t, int>, qmr::DensePlan> dense_plans;
     // Workspace of the wide-block kernel: the activation images.
     unsigned char *ws_wide = nullptr;
     size_t ws_wide_bytes = 0;
@@ -504,6 +507,77 @@ hipError_t launch_split_k(qmr_device *dev, const qmr::AffineArgs &a, const qmr::
     return e;
 }
 
+// The dense matrix-core kernel's plan for a view it supports, honouring a
+// forced shape (rr == -5, ks = ring*10000 + kw*1000 + rt*100 + ns; zero
+// fields leave them to its planner). rt == 0 sends the product to the
+// vector-ALU kernels: when the hook asks for them (rr == -1), when the view
+// is not supported, and by default for one RHS (where the streaming kernel
+// is within 6% of the best matrix-core plan on the decoder's shapes and
+// faster on most) or when the planner's estimate is not below the
+// vector-ALU kernel's (small matrices, whose fixed costs dominate).
+qmr::DensePlan dense_plan(const qmr_device *dev, const uint16_t *w, uint32_t rows, uint32_t cols,
+                          uint32_t batch) {
+    const qmr::GemvPlan f = dev->forced_plan;
+    if (f.rr == -1 || !qmr::dense_mfma_supported(w, rows, cols, batch)) return qmr::DensePlan{};
+    if (f.rr != -5 && batch == 1) return qmr::DensePlan{};
+    const int ks = f.rr == -5 ? f.ks : 0;
+    const auto key = std::make_tuple(rows, cols, batch, f.rr == -5 ? ks : -1);
+    const auto it = dev->dense_plans.find(key);
+    if (it != dev->dense_plans.end()) return it->second;
+    qmr::DenseForce force;
+    force.ring = uint32_t(ks / 10000 % 10);
+    force.kw = uint32_t(ks / 1000 % 10);
+    force.rt = uint32_t(ks / 100 % 10);
+    force.ns = uint32_t(ks % 100);
+    qmr::DensePlan pl = qmr::plan_dense_mfma(rows, cols, batch, dev->limits, force);
+    if (f.rr != -5 && pl.rt > 0 && !(pl.cost_us < qmr::dense_valu_cost(rows, cols, batch))) pl = qmr::DensePlan{};
+    if (dev->dense_plans.size() > 4096) dev->dense_plans.clear();
+    dev->dense_plans.emplace(key, pl);
+    return pl;
+}
+
+// Dense F16 matvec / block: the matrix-core kernel where it has a plan
+// (its split sums in the device's slot workspace, or with `fixed` in the
+// static scratch, whose region its finishers leave zero), else the
+// vector-ALU kernels, which need no workspace; so does a static launch
+// whose plan's sums would not fit the static scratch.
+hipError_t launch_dense(qmr_device *dev, const uint16_t *w, const float *x, float *y, uint32_t rows, uint32_t cols,
+                        uint32_t batch, unsigned char *fixed) {
+    const qmr::DensePlan pl = dense_plan(dev, w, rows, cols, batch);
+    const size_t need = pl.rt > 0 ? qmr::dense_mfma_workspace(pl, rows, batch) : 0;
+    const size_t part = (need + 255) / 256 * 256;
+    const size_t extent = pl.ns > 1 ? part + size_t(pl.nbands) * sizeof(uint32_t) : 0;
+    if (pl.rt == 0 || (fixed && extent > QMR_STATIC_SCRATCH_BYTES)) {
+        dev->last_hip = "dense_f16_kernel";
+        start_gpu(dev);
+        return qmr::launch_dense_f16(w, x, y, rows, cols, batch, dev->stream);
+    }
+    dev->last_hip = "dense_mfma_kernel ring=" + std::to_string(pl.ring) + " kw=" + std::to_string(pl.kw) +
+                    " rt=" + std::to_string(pl.rt) + " ns=" + std::to_string(pl.ns);
+    qmr::TileWait wait;
+    wait.status = dev->status_dev;
+    wait.force_give_up = dev->force_give_up;
+    if (pl.ns == 1) {
+        start_gpu(dev);
+        return qmr::launch_dense_mfma(w, x, y, rows, cols, batch, pl, nullptr, nullptr, 1u, wait, dev->stream);
+    }
+    if (!fixed) {
+        const uint32_t epoch = next_slot_epoch(dev, need);
+        ensure_counters(dev, pl.nbands);
+        start_gpu(dev);
+        return qmr::launch_dense_mfma(w, x, y, rows, cols, batch, pl, dev->ws_slots, dev->ws_counters, epoch, wait,
+                                      dev->stream);
+    }
+    start_gpu(dev);
+    hipError_t e = clear_static_slots(dev, fixed, (extent + 3) / 4 * 4);
+    if (e != hipSuccess) return e;
+    wait.reset_slots = true;
+    e = qmr::launch_dense_mfma(w, x, y, rows, cols, batch, pl, reinterpret_cast<unsigned long long *>(fixed),
+                               reinterpret_cast<uint32_t *>(fixed + part), 1u, wait, dev->stream);
+    if (e != hipSuccess) mark_static_dirty(dev, extent);
+    return e;
+}
+
 // One packed-affine product of at most four RHS: the row-band matrix-core
 // kernel where it has a plan whose workgroups are all resident at once; else
 // the split-K matrix-core kernel where it supports the format, unless
@@ -884,13 +958,16 @@ int qmr_command_finish(qmr_command *command, qmr_frame_timing *timing) {
         if (status != 0) {
             __atomic_store_n(dev->status_host, 0u, __ATOMIC_RELEASE);
             mark_static_dirty(dev, QMR_STATIC_SCRATCH_BYTES);
-            const bool split_k = (status & 0x40000000u) != 0;
+            const bool band_kernel = (status & 0x60000000u) == 0;
+            const char *kernel = (status & 0x40000000u) ? "affine_mfma_kernel"
+                                 : (status & 0x20000000u) ? "dense_mfma_kernel"
+                                                           : "affine_band_kernel";
             throw Error{QMR_ERR_DEVICE,
-                        std::string("GPU command failed: ") + (split_k ? "affine_mfma_kernel" : "affine_band_kernel") +
-                            " band " + std::to_string(status & 0x3FFFFFFFu) +
-                            (split_k ? ": the last K split gave up waiting for the other splits' tagged sums"
-                                     : ": the last K split gave up waiting for the other splits' sums (the band's "
-                                       "workgroups were not all resident at once)") +
+                        std::string("GPU command failed: ") + kernel + " band " +
+                            std::to_string(status & 0x1FFFFFFFu) +
+                            (band_kernel ? ": the last K split gave up waiting for the other splits' sums (the band's "
+                                           "workgroups were not all resident at once)"
+                                         : ": the last K split gave up waiting for the other splits' tagged sums") +
                             "; the command's outputs are not valid"};
         }
         float ms = 0.f;
@@ -1047,12 +1124,9 @@ static int encode_command(qmr_command *command, const char *cname, qmr_buffer *c
             e = qmr::launch_embed_f16(reinterpret_cast<const uint16_t *>(ptr(0)), params[0],
                                       params[1], reinterpret_cast<float *>(ptr(1)), dev->stream);
         } else if (name == "matvec_f16" || name == "matmul_f16") {
-            start_gpu(dev);
             const uint32_t batch = name == "matmul_f16" ? params[2] : 1;
-            e = qmr::launch_dense_f16(reinterpret_cast<const uint16_t *>(ptr(0)),
-                                      reinterpret_cast<const float *>(ptr(1)),
-                                      reinterpret_cast<float *>(ptr(2)), params[0], params[1],
-                                      batch, dev->stream);
+            e = launch_dense(dev, reinterpret_cast<const uint16_t *>(ptr(0)), reinterpret_cast<const float *>(ptr(1)),
+                             reinterpret_cast<float *>(ptr(2)), params[0], params[1], batch, fixed);
         } else if (fused) {
             qmr::AffineArgs a{};
             a.rows = params[0];
@@ -1307,6 +1381,16 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
                   uint32_t batch, int *rr, int *ks) {
     return guarded([&]() -> int {
         ensure(device != nullptr, "null device");
+        if (bits == 16) {
+            // Dense F16 (an aligned view): rr = -5, ks = ring*10000 +
+            // kw*1000 + rt*100 + ns on the matrix-core kernel, else rr = -1
+            // (vector-ALU kernels).
+            const qmr::DensePlan pl =
+                dense_plan(device, reinterpret_cast<const uint16_t *>(uintptr_t(256)), rows, cols, batch);
+            if (rr) *rr = pl.rt > 0 ? -5 : -1;
+            if (ks) *ks = pl.rt > 0 ? int(pl.ring * 10000 + pl.kw * 1000 + pl.rt * 100 + pl.ns) : 0;
+            return QMR_OK;
+        }
         qmr::AffineArgs a{};
         a.rows = rows;
         a.cols = cols;

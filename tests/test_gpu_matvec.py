@@ -288,16 +288,18 @@ def test_matrix_core_kernels_read_x_at_4_byte_offsets(gpu, rr, name, batch):
     assert_gate(got[1:batch * rows + 1], want, f"{name} B{batch} x at a 4-byte offset")
 
 
+@pytest.mark.parametrize("plan", [(0, 0), (-1, 0)])
 @pytest.mark.parametrize("rows,cols,batch", [
     (5120, 17408, 1), (17408, 5120, 3), (5120, 17408, 4), (301, 4104, 2), (4099, 2056, 3), (1000, 8, 4),
     (77, 1001, 1), (33, 512, 4)])
-def test_dense_f16_products_at_scale(gpu, rows, cols, batch):
+def test_dense_f16_products_at_scale(gpu, rows, cols, batch, plan):
     """matvec_f16 / matmul_f16 (kernels/qwen.metal:48-57,
-    kernels/matmul_block.metal:213-248) against the FP64 oracle: the
-    streaming kernel (cols % 8 == 0, any row tail, 1-4 RHS) in its three
-    shapes (four waves splitting K over 4 or 8 rows, one wave per 4 rows at
-    17408x5120 B=3; partial last steps and row groups), and the simple
-    kernel (cols % 8 != 0)."""
+    kernels/matmul_block.metal:213-248) against the FP64 oracle: the default
+    choice (the matrix-core kernel for some products of 2-4 RHS), and with
+    the rr = -1 hook the vector-ALU streaming kernel (cols % 8 == 0, any row
+    tail, 1-4 RHS) in its three shapes (four waves splitting K over 4 or 8
+    rows, one wave per 4 rows at 17408x5120 B=3; partial last steps and row
+    groups); the simple kernel takes cols % 8 != 0 either way."""
     rng = np.random.default_rng(rows * 3 + cols + batch)
     w16 = rng.standard_normal(rows * cols).astype(np.float16).view(np.uint16)
     x = rng.standard_normal((batch, cols)).astype(np.float32)
@@ -305,7 +307,13 @@ def test_dense_f16_products_at_scale(gpu, rows, cols, batch):
     xb = gpu.upload_f32(x.ravel())
     yb = gpu.upload_f32(np.full(batch * rows + 1, 7.0, np.float32))
     name = "matvec_f16" if batch == 1 else "matmul_f16"
-    gpu.dispatch(name, [wb, xb, yb], [rows, cols] + ([batch] if batch > 1 else []))
+    gpu.set_gemv_plan(*plan)
+    try:
+        gpu.dispatch(name, [wb, xb, yb], [rows, cols] + ([batch] if batch > 1 else []))
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    if plan == (-1, 0) or cols % 32 != 0:
+        assert gpu.last_hip_kernel() == "dense_f16_kernel", gpu.last_hip_kernel()
     got = gpu.read_f32(yb, batch * rows + 1)
     assert got[-1] == 7.0, "wrote past y"
     want = oracle.dense_f16_f64(w16, x, rows, cols, batch)

@@ -6,7 +6,8 @@ writes NaN for the band and sets the device's status word, and
 qmr_command_finish returns QMR_ERR_DEVICE naming the kernel and band, as the
 reference fails a frame whose Metal command buffer did not complete
 (src/gpu.rs:861-865). The split-K kernel's last arriver waits the same way
-for each partial's epoch tag and reports the same way.
+for each partial's epoch tag and reports the same way, and so does the dense
+F16 matrix-core kernel's.
 
 The give-up is forced from the host (qmr_set_band_wait_fault: the last
 arrivers wait for a tag that no split of the launch publishes, with a short
@@ -28,6 +29,11 @@ pytestmark = pytest.mark.gpu
 
 
 def _inputs(rng, rows, cols, batch, form):
+    if form == "dense":
+        w16 = rng.standard_normal(rows * cols).astype(np.float16).view(np.uint16)
+        x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
+        want = oracle.dense_f16_f64(w16, x, rows, cols, batch)
+        return "matmul_f16", [w16, x.ravel()], [rows, cols, batch], want
     m = _matrix(rng, rows, cols)
     x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
     if form == "mlp":
@@ -59,6 +65,7 @@ def _command(gpu, name, bufs, params, static):
     (5120, 17408, 3, "plain", (-2, 4), "affine_mfma_kernel"),     # split-K, four K splits
     (4096, 2048, 3, "mlp", (-2, 0), "affine_mfma_kernel"),        # split-K's MLP form
     (40960, 2048, 2, "plain", (-4, 240801), "affine_band_kernel"),  # elected finishers, several rounds
+    (5120, 17408, 3, "dense", (-5, 408), "dense_mfma_kernel"),    # dense F16, eight K splits
 ])
 def test_give_up_fails_the_command_and_the_next_one_succeeds(gpu, static, rows, cols, batch, form, plan, kernel):
     rng = np.random.default_rng([rows, cols, batch, int(static)])
