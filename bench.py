@@ -395,7 +395,8 @@ def bench_dense(gpu: qmr.Gpu, args) -> list:
     """Dense F16 products at the 27B MLP shapes (matvec_f16 / matmul_f16,
     kernels/qwen.metal:48-57, kernels/matmul_block.metal:213-248), for
     checkpoints without quantisation: 178 MB of F16 weights, 3 rotating
-    copies, B=1 and B=3."""
+    copies, B=1 and B=3, with the kernel the default choice ran; at B=3 the
+    vector-ALU kernel is timed beside it (the rr = -1 hook)."""
     out = []
     for tag in ("down", "gate_up"):
         rows, cols = synth.MLP_SHAPES[tag]
@@ -407,16 +408,25 @@ def bench_dense(gpu: qmr.Gpu, args) -> list:
             ys = [gpu.alloc_f32(batch * rows) for _ in ws]
             name = "matvec_f16" if batch == 1 else "matmul_f16"
             params = [rows, cols] + ([batch] if batch > 1 else [])
-            mean_ms, _, _ = time_kernel(gpu, name, [[w, xb, y] for w, y in zip(ws, ys)], params,
-                                        args.config3_steps, 6)
+            bufs = [[w, xb, y] for w, y in zip(ws, ys)]
+            mean_ms, _, _ = time_kernel(gpu, name, bufs, params, args.config3_steps, 6)
+            kernel = gpu.last_hip_kernel()
             nbytes = rows * cols * 2 + 4 * batch * (rows + cols)
             gbps = nbytes / (mean_ms * 1e-3) / 1e9
-            r = {"shape": f"{rows}x{cols}", "batch": batch, "name": name, "us_mean": round(mean_ms * 1e3, 2),
-                 "algorithmic_bytes": nbytes,
+            r = {"shape": f"{rows}x{cols}", "batch": batch, "name": name, "kernel": kernel,
+                 "us_mean": round(mean_ms * 1e3, 2), "algorithmic_bytes": nbytes,
                  "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                               "frac": round(gbps / HBM_PEAK_GBS, 4)}}
-            log(f"bench: dense F16 {rows}x{cols} B={batch}: {r['us_mean']} us, {r['roofline']['achieved']} GB/s "
-                f"= {100 * r['roofline']['frac']:.1f}% of peak")
+            if batch > 1:
+                gpu.set_gemv_plan(-1, 0)
+                try:
+                    valu_ms, _, _ = time_kernel(gpu, name, bufs, params, args.config3_steps, 6)
+                finally:
+                    gpu.set_gemv_plan(0, 0)
+                r["us_vector_alu"] = round(valu_ms * 1e3, 2)
+            log(f"bench: dense F16 {rows}x{cols} B={batch} ({kernel}): {r['us_mean']} us, "
+                f"{r['roofline']['achieved']} GB/s = {100 * r['roofline']['frac']:.1f}% of peak"
+                + (f"; vector-ALU kernel {r['us_vector_alu']} us" if batch > 1 else ""))
             out.append(r)
         del ws
     return out
