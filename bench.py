@@ -817,6 +817,8 @@ def main() -> int:
                     help="time only the 5120x17408 shapes (for profiling runs)")
     ap.add_argument("--only-wide", action="store_true",
                     help="time only the config-4 wide block (for profiling runs)")
+    ap.add_argument("--only-dense", action="store_true",
+                    help="only time the dense F16 products (for profiling), print that JSON and exit")
     ap.add_argument("--wide-steps", type=int, default=30)
     ap.add_argument("--config3-steps", type=int, default=60)
     ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
@@ -858,6 +860,10 @@ def main() -> int:
         copy_calibration(gpu, args.copy_calibration, 8)
     if args.floor_sweep:
         print(json.dumps({"floor_sweep": floor_sweep(gpu, args)}), flush=True)
+        gpu.close()
+        return 0
+    if args.only_dense:
+        print(json.dumps({"dense_f16": bench_dense(gpu, args)}), flush=True)
         gpu.close()
         return 0
     shapes = [] if args.only_wide else [("down", synth.MLP_SHAPES["down"])]
