@@ -241,6 +241,27 @@ def test_static_scratch_is_bit_identical_twice_in_a_row(gpu):
         assert_gate(got, oracle.dense_f16_f64(w16, x, rows, cols, batch), f"static {k1}")
 
 
+def test_static_scratch_too_small_for_the_split_sums_takes_the_vector_alu_kernel(gpu):
+    """A plan whose split sums exceed the static scratch (here eight splits
+    of 4 x 65536 outputs: 16.8 MB against 8 MiB) runs, under
+    qmr_encode_static, on the vector-ALU kernel, which needs no workspace;
+    qmr_encode keeps the matrix-core plan. Both meet the gate."""
+    rows, cols, batch = 65536, 2048, 4
+    rng = np.random.default_rng(21)
+    w16, x = _dense(rng, rows, cols, batch)
+    want = oracle.dense_f16_f64(w16, x, rows, cols, batch)
+    gpu.set_gemv_plan(-5, 408)
+    try:
+        got, kernel = _run(gpu, w16, x, rows, cols, batch)
+        assert kernel.startswith("dense_mfma_kernel") and kernel.endswith(" rt=4 ns=8"), kernel
+        assert_gate(got, want, "dense 8 splits, qmr_encode")
+        got, kernel = _run(gpu, w16, x, rows, cols, batch, static=True)
+        assert kernel == "dense_f16_kernel", kernel
+        assert_gate(got, want, "dense, qmr_encode_static fallback")
+    finally:
+        gpu.set_gemv_plan(0, 0)
+
+
 def test_repeated_launches_reuse_slots(gpu):
     """Split plans tag their sums with a new epoch per launch over the same
     slot workspace: repeated launches with different inputs each give their

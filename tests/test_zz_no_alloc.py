@@ -1,7 +1,8 @@
 """qmr_encode_static, the no-allocation variant of qmr_encode, on the GPU
 through the C ABI. Each kernel family whose launches take workspace (the
 row-band kernel's split sums, the split-K kernel's partial sums and counters
-in the plain, residual and MLP forms, the wide block's activation images) is
+in the plain, residual and MLP forms, the wide block's activation images,
+the dense F16 matrix-core kernel's split sums and counters) is
 run twice in a row through qmr_encode_static, the second call on a smaller
 input so that it finds the first call's contents in the shared scratch, and
 each output is compared with qmr_encode's on the same inputs (same plan, so
@@ -36,6 +37,13 @@ def _matrix(rng, rows, cols):
 
 def _case(rng, form, rows, cols, batch):
     """Inputs of one launch: (name, host arrays in buffer order, params, FP64 oracle)."""
+    if form == "dense":
+        w16 = rng.standard_normal(rows * cols).astype(np.float16).view(np.uint16)
+        x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
+        want = oracle.dense_f16_f64(w16, x, rows, cols, batch)
+        if batch == 1:
+            return "matvec_f16", [w16, x.ravel()], [rows, cols], want
+        return "matmul_f16", [w16, x.ravel()], [rows, cols, batch], want
     m = _matrix(rng, rows, cols)
     x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
     params = [rows, cols, 4, 64, batch]
@@ -83,6 +91,8 @@ CASES = [
     ("mlp", (0, 0), (4096, 2048, 3), (512, 1024, 1), "affine_band_kernel"),          # gate and up sums
     ("mlp", (-2, 0), (4096, 2048, 3), (512, 1024, 1), "affine_mfma_kernel (MLP)"),
     ("wide", (0, 0), (2048, 5120, 64), (512, 2048, 16), "wide_mfma_kernel"),         # activation images
+    ("dense", (0, 0), (5120, 17408, 3), (2048, 8192, 2), "dense_mfma_kernel"),       # dense F16 split sums
+    ("dense", (-5, 408), (17408, 5120, 4), (1000, 4096, 2), "dense_mfma_kernel"),
 ]
 
 
@@ -140,7 +150,10 @@ def test_static_band_slots_stay_clear_across_a_sequence_of_calls(gpu):
            ("plain", (0, 0), (5120, 17408, 3)),
            # Elected finishers: slots of every split, then the arrival counters.
            ("plain", (-4, 240801), (40960, 2048, 2)), ("plain", (-4, 240801), (40960, 2048, 2)),
-           ("plain", (0, 0), (5120, 17408, 1))]
+           ("plain", (0, 0), (5120, 17408, 1)),
+           # Dense F16 split sums after an MLP form left its slots, then the band.
+           ("mlp", (-4, 220202), (4096, 2048, 3)), ("dense", (-5, 408), (5120, 17408, 3)),
+           ("dense", (0, 0), (17408, 5120, 2)), ("plain", (0, 0), (5120, 17408, 3))]
     fresh = qmr.Gpu("aligned")
     try:
         for form, plan, (rows, cols, batch) in seq:
