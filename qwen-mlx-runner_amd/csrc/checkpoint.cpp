@@ -26,6 +26,7 @@
 #include <optional>
 #include <set>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <utility>
 #include <vector>
@@ -862,10 +863,32 @@ void release_matrix(qmr_matrix *m) {
 }
 
 void upload(qmr_device *device, const void *data, size_t bytes, qmr_buffer **out) {
-    // Large arrays (the codes) go through the pinned staging path.
+    // Large arrays go through the pinned staging path.
     const int rc = bytes >= (size_t(32) << 20) ? qmr::upload_staged(device, data, bytes, out)
                                                : qmr_buffer_upload(device, data, bytes, out);
     if (rc != QMR_OK) throw Error{QMR_ERR_DEVICE, qmr_last_error()};
+}
+
+// A packed matrix's codes, scales and biases through one staged pipeline.
+void upload_matrix(qmr_device *device, const void *w, size_t w_bytes, const void *s, const void *b,
+                   size_t meta_bytes, qmr_matrix *m) {
+    const qmr::StagedView views[3] = {{w, w_bytes}, {s, meta_bytes}, {b, meta_bytes}};
+    qmr_buffer *out[3] = {nullptr, nullptr, nullptr};
+    if (qmr::upload_staged_views(device, views, 3, out) != QMR_OK) throw Error{QMR_ERR_DEVICE, qmr_last_error()};
+    m->weight = out[0];
+    m->scales = out[1];
+    m->biases = out[2];
+}
+
+// Whether n BF16 values are all finite (the exponent field not all ones).
+bool bf16_all_finite(const unsigned char *p, size_t n) {
+    uint16_t bad = 0;
+    for (size_t i = 0; i < n; ++i) {
+        uint16_t v;
+        std::memcpy(&v, p + 2 * i, 2);
+        bad |= uint16_t((v & 0x7F80u) == 0x7F80u);
+    }
+    return bad == 0;
 }
 
 }  // namespace
@@ -964,17 +987,27 @@ int qmr_matrix_load(qmr_device *device, const qmr_checkpoint *checkpoint, const 
             // are uploaded as they are once no value is Inf or NaN.
             const size_t n = qmr_checkpoint::elements(*r.s);
             const std::string module = r.key.substr(0, r.key.size() - 7);
-            for (const auto &part : {std::make_pair(r.s, ".scales"), std::make_pair(r.b, ".biases")}) {
-                const unsigned char *p = checkpoint->bytes(*part.first);
-                bool finite = true;
-                for (size_t i = 0; i < n; ++i) finite &= (p[2 * i + 1] & 0x7f) != 0x7f || (p[2 * i] & 0x80) == 0;
-                ensure(finite, module + part.second + " contains non-finite values");
-            }
             ensure(r.w->length + 2 * n * 2 < qmr::device_free_bytes(device),
                    "model exceeds the device's free memory; use packed 4-bit weights");
-            upload(device, checkpoint->bytes(*r.w), r.w->length, &m.weight);
-            upload(device, checkpoint->bytes(*r.s), n * 2, &m.scales);
-            upload(device, checkpoint->bytes(*r.b), n * 2, &m.biases);
+            // The finiteness checks run on another thread while the arrays
+            // upload; a non-finite value releases the buffers and fails the
+            // load with the check's message, as before any upload.
+            const unsigned char *sp = checkpoint->bytes(*r.s);
+            const unsigned char *bp = checkpoint->bytes(*r.b);
+            bool s_ok = true, b_ok = true;
+            std::thread check([&] {
+                s_ok = bf16_all_finite(sp, n);
+                b_ok = bf16_all_finite(bp, n);
+            });
+            try {
+                upload_matrix(device, checkpoint->bytes(*r.w), r.w->length, sp, bp, n * 2, &m);
+            } catch (...) {
+                check.join();
+                throw;
+            }
+            check.join();
+            ensure(s_ok, module + ".scales contains non-finite values");
+            ensure(b_ok, module + ".biases contains non-finite values");
             qmr_record_compacted_metadata(device, uint64_t(n) * 2 * 2);
             m.metadata_bf16 = 1;
         } else {
@@ -989,14 +1022,11 @@ int qmr_matrix_load(qmr_device *device, const qmr_checkpoint *checkpoint, const 
             const size_t meta_bytes = compacted ? 2 * n * 2 : 2 * n * 4;
             ensure(r.w->length + meta_bytes < qmr::device_free_bytes(device),
                    "model exceeds the device's free memory; use packed 4-bit weights");
-            upload(device, checkpoint->bytes(*r.w), r.w->length, &m.weight);
             if (compacted) {
-                upload(device, s16.data(), n * 2, &m.scales);
-                upload(device, b16.data(), n * 2, &m.biases);
+                upload_matrix(device, checkpoint->bytes(*r.w), r.w->length, s16.data(), b16.data(), n * 2, &m);
                 qmr_record_compacted_metadata(device, uint64_t(n) * 2 * 2);
             } else {
-                upload(device, s.data(), n * 4, &m.scales);
-                upload(device, b.data(), n * 4, &m.biases);
+                upload_matrix(device, checkpoint->bytes(*r.w), r.w->length, s.data(), b.data(), n * 4, &m);
             }
             m.metadata_bf16 = compacted ? 1 : 0;
         }

@@ -31,9 +31,17 @@ void clear_error();
 // throws Error on a HIP failure.
 size_t device_free_bytes(const ::qmr_device *device);
 
-// Uploads `bytes` from a large pageable source (a mapped checkpoint shard)
-// into a new device buffer through pinned staging buffers filled by several
-// host threads; returns QMR_OK or an error status with qmr_last_error() set.
+// Uploads from large pageable sources (mapped checkpoint shards) into new
+// device buffers through pinned staging slots filled by several host
+// threads, all views in one pipeline; returns QMR_OK or an error status with
+// qmr_last_error() set (then no buffer is returned).
+constexpr int kStageSlots = 3;
+constexpr size_t kStageChunk = size_t(8) << 20;
+struct StagedView {
+    const void *src;
+    size_t bytes;
+};
+int upload_staged_views(::qmr_device *device, const StagedView *views, size_t n, ::qmr_buffer **outs);
 int upload_staged(::qmr_device *device, const void *src, size_t bytes, ::qmr_buffer **out);
 
 enum class BlockMatmulMode : int { Legacy = 0, Shared = 1, MlpR2 = 2 };

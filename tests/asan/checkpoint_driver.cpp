@@ -20,6 +20,7 @@ int record_error(int code, const std::string &message) {
 void clear_error() { g_error.clear(); }
 size_t device_free_bytes(const ::qmr_device *) { return 0; }
 int upload_staged(::qmr_device *, const void *, size_t, ::qmr_buffer **) { return QMR_ERR_DEVICE; }
+int upload_staged_views(::qmr_device *, const StagedView *, size_t, ::qmr_buffer **) { return QMR_ERR_DEVICE; }
 }  // namespace qmr
 extern "C" {
 const char *qmr_last_error(void) { return g_error.c_str(); }
