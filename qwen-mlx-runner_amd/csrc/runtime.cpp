@@ -182,16 +182,14 @@ namespace {
 class CopyCrew {
 public:
     explicit CopyCrew(unsigned n) : n_(n) {
-        for (unsigned t = 1; t < n_; ++t) threads_.emplace_back([this, t] { run(t); });
-    }
-    ~CopyCrew() {
-        {
-            std::lock_guard<std::mutex> lock(mu_);
-            quit_ = true;
+        try {
+            for (unsigned t = 1; t < n_; ++t) threads_.emplace_back([this, t] { run(t); });
+        } catch (...) {
+            stop();  // threads already started must not outlive a crew that failed to form
+            throw;
         }
-        go_.notify_all();
-        for (auto &t : threads_) t.join();
     }
+    ~CopyCrew() { stop(); }
     void copy(unsigned char *dst, const unsigned char *src, size_t len) {
         {
             std::lock_guard<std::mutex> lock(mu_);
@@ -208,6 +206,15 @@ public:
     }
 
 private:
+    void stop() {
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            quit_ = true;
+        }
+        go_.notify_all();
+        for (auto &t : threads_) t.join();
+        threads_.clear();
+    }
     void share(unsigned t, unsigned char *dst, const unsigned char *src, size_t len) const {
         const size_t part = (len + n_ - 1) / n_;
         const size_t b = size_t(t) * part;
