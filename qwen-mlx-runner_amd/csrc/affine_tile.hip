@@ -97,6 +97,11 @@ struct BandParams {
     uint32_t split_e[5];  // first entry of each split, then n_entries (host_split_begin)
     uint32_t kw_shift;    // log2(kw)
     uint32_t unit_shift;  // log2 of the threads per row in the metadata loads (>= units per row)
+    // Two-phase x staging (single-split plans with one wave per tile): the
+    // images of the K tiles [0, phase_tiles) are staged first and those of
+    // [phase_tiles, tiles) replace them once every wave has consumed entry
+    // phase_entry - 1, so a workgroup holds half the images in LDS.
+    uint32_t phase_entry, phase_tiles;
 };
 
 // Launches the plan's instance of format <BITS, META> (META 0 f32, 1 bf16,
@@ -104,11 +109,12 @@ struct BandParams {
 template <int BITS, int META>
 hipError_t launch_meta(const BandParams &p, const TilePlan &pl, uint32_t group, uint32_t batch, hipStream_t stream);
 
-// The kernel instance for a format, x-item count, ring depth and form
-// (plain or the MLP form; the residual form's resources are the plain's),
-// for occupancy queries; null for a batch the group size does not allow.
+// The kernel instance for a format, x-item count, ring depth, form (plain
+// or the MLP form; the residual form's resources are the plain's) and x
+// staging phases (1, or 2 for the plain form), for occupancy queries; null
+// for a batch the group size does not allow.
 template <int BITS, int META>
-const void *instance_meta(uint32_t group, uint32_t batch, uint32_t xi, uint32_t ring, bool mlp);
+const void *instance_meta(uint32_t group, uint32_t batch, uint32_t xi, uint32_t ring, bool mlp, uint32_t phases);
 
 }  // namespace band
 
@@ -128,9 +134,13 @@ constexpr int kMetaUnits = 4;  // 16-byte metadata loads per thread and plane (f
 // weights) serves both; the band's last split adds each row's gate and up
 // sums in split order and applies 1/rms (the products are linear in it) and
 // SwiGLU.
-template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE>
+// PH = 2: the two-phase x staging of BandParams (plain and residual forms,
+// plans of one split and one wave per tile, so every wave streams the same
+// entries and meets the phase barriers together).
+template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE, int PH>
 __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) {
     constexpr bool MLP = FUSE == 2;
+    static_assert(PH == 1 || (PH == 2 && !MLP), "two-phase staging serves the plain and residual forms");
     constexpr int NGM = kTileK / GROUP;  // quant groups per tile
     constexpr int SLOTS = 16 / NGM;      // A rows per quant group
     constexpr int HALF = SLOTS / 2;      // RHS per quant group in D (>= B)
@@ -209,7 +219,11 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     // queues its loads behind those of the workgroups dispatched before it on
     // its CU, and nothing can be multiplied before x is staged. Item it = ((Tl*B + t)*4 + g)*4 + m covers the 8
     // columns (ST0 + Tl)*128 + 32g + 8m of RHS t (mfma_common.hpp). ----
-    const uint32_t items = nT * B * 16u;
+    // Tiles whose images the first phase stages; with PH = 2 the rest follow
+    // in the second phase into the same LDS, whose capacity is the larger.
+    const uint32_t nT1 = PH == 2 ? min(p.phase_tiles, nT) : nT;
+    const uint32_t nTimg = PH == 2 ? max(nT1, nT - nT1) : nT;
+    const uint32_t items = nT1 * B * 16u;
     float xv[XI][8];
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
@@ -315,7 +329,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     // first and comes from L2, while the metadata behind it comes from HBM.
     // ----
     u4 *imgA = reinterpret_cast<u4 *>(img);
-    float4 *imgS = reinterpret_cast<float4 *>(img + nT * TIMG_A);
+    float4 *imgS = reinterpret_cast<float4 *>(img + nTimg * TIMG_A);
     // MLP: each x[t]'s sum of squares over the split's columns, from the
     // staged items (items past the split read zeros), for 1/rms at the end.
     [[maybe_unused]] float xsq[MLP ? B : 1] = {};
@@ -430,7 +444,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     }
 
     // Zero sums and factors of absent RHS.
-    stage_x_pads<GROUP, B>(nT, tid, nthr, imgS);
+    stage_x_pads<GROUP, B>(nT1, tid, nthr, imgS);
     lds_barrier();
 
     // ---- 6. Stream the wave's entries. ----
@@ -439,11 +453,15 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const uint32_t m_row = (ti * 16u + uint32_t(r)) * Gp + uint32_t(L.gD);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     h8 a[4] = {h8{}, h8{}, h8{}, h8{}};
+    // The images of the current phase start at tile img_base (0, or nT1 in
+    // the second phase of PH = 2); the metadata covers the whole split.
+    uint32_t img_base = 0;
     auto compute = [&](const u4 (&c)[NLD], uint32_t Tl) {
         float sv, bv;
         meta_entry<META>(ldsM + (m_row + Tl * NGM) * (META == 0 ? 2 : 1), sv, bv);
-        const float4 sx = imgS[(Tl * NGM + L.gD) * (HALF / 2) + t0 / 2];
-        tile_product<BITS, META, GROUP, B>(c, L, imgA + Tl * 4 * (8 * B), sv, bv, sx, a, acc);
+        const uint32_t Ti = Tl - img_base;
+        const float4 sx = imgS[(Ti * NGM + L.gD) * (HALF / 2) + t0 / 2];
+        tile_product<BITS, META, GROUP, B>(c, L, imgA + Ti * 4 * (8 * B), sv, bv, sx, a, acc);
     };
     auto exchange = [&](const u4 (&c)[2], u4 &kept, u4 &got) {
         u4 send;
@@ -456,7 +474,11 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         for (int d = 0; d < 4; ++d) got[d] = uint32_t(__builtin_amdgcn_mov_dpp(int(send[d]), 0x128, 0xF, 0xF, false));
     };
     const uint32_t nE = E1 - E0;
-    for (uint32_t base = 0; base < nE; base += P) {
+    // One pass of the ring: the P entries from `base`, each multiplied once
+    // landed and its slot refilled with the entry P further on. Every pass
+    // issues the same loads, so the wait before each entry's product counts
+    // only the loads behind it.
+    auto pass = [&](uint32_t base) {
 #pragma unroll
         for (int j = 0; j < P; ++j) {
             const uint32_t i = base + j;
@@ -481,6 +503,40 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
             issue(ring[j], E0 + i + P);
             __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    if constexpr (PH == 2) {
+        // Two phases (every wave streams the same entries, so all meet the
+        // barriers together). phase_entry is a multiple of P inside the
+        // stream: the first phase ends with a whole pass, before which x of
+        // tiles [nT1, nT) is requested, so it lands behind the ring's loads
+        // without waiting for them. Once every wave has multiplied its last
+        // first-phase entry, those x images replace the first phase's.
+        const uint32_t pe = p.phase_entry;
+        uint32_t base = 0;
+        for (; base + P < pe; base += P) pass(base);
+        const uint32_t items2 = (nT - nT1) * B * 16u;
+        float x2[XI][8];
+#pragma unroll
+        for (int i2 = 0; i2 < XI; ++i2) {
+            const uint32_t it = uint32_t(tid) + uint32_t(i2 * nthr);
+            load_x8(x2[i2], xr, uint32_t(item_pos<B>(it).t), (ST0 + nT1) * kTileK + item_col<B>(it), p.cols,
+                    it < items2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        pass(base);
+        lds_barrier();
+#pragma unroll
+        for (int i2 = 0; i2 < XI; ++i2) {
+            const uint32_t it = uint32_t(tid) + uint32_t(i2 * nthr);
+            if (i2 > 0 && uint32_t(tid) - uint32_t(lane) + uint32_t(i2 * nthr) >= items2) break;
+            stage_x_item<BITS, GROUP, B>(x2[i2], it, it < items2, lane, imgA, imgS);
+        }
+        stage_x_pads<GROUP, B>(nT - nT1, tid, nthr, imgS);
+        lds_barrier();
+        img_base = nT1;
+        for (base = pe; base < nE; base += P) pass(base);
+    } else {
+        for (uint32_t base = 0; base < nE; base += P) pass(base);
     }
 
     // ---- 7. Combine hi/lo slots and quant groups, add the KW partial sums
@@ -635,9 +691,9 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     }
 }
 
-template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE>
+template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE, int PH>
 hipError_t launch_inst(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
-    auto kernel = affine_band_kernel<BITS, META, GROUP, B, XI, P, FUSE>;
+    auto kernel = affine_band_kernel<BITS, META, GROUP, B, XI, P, FUSE, PH>;
     if (pl.lds > 65536) {
         const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kernel), pl.lds);
         if (e != hipSuccess) return e;
@@ -649,14 +705,23 @@ hipError_t launch_inst(const BandParams &p, const TilePlan &pl, hipStream_t stre
 template <int BITS, int META, int GROUP, int B, int XI>
 hipError_t launch_xi(const BandParams &p, const TilePlan &pl, hipStream_t stream) {
     const int fuse = p.w2 != nullptr ? 2 : p.r != nullptr ? 1 : 0;
-    if (pl.ring >= 3) {
-        if (fuse == 2) return launch_inst<BITS, META, GROUP, B, XI, 3, 2>(p, pl, stream);
-        return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 3, 1>(p, pl, stream)
-                         : launch_inst<BITS, META, GROUP, B, XI, 3, 0>(p, pl, stream);
+    if (pl.phases == 2) {
+        // Every wave must stream the same entries to meet the phase barriers.
+        if (fuse == 2 || pl.ns != 1 || pl.kw != 1) return hipErrorInvalidValue;
+        if (pl.ring >= 3)
+            return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 3, 1, 2>(p, pl, stream)
+                             : launch_inst<BITS, META, GROUP, B, XI, 3, 0, 2>(p, pl, stream);
+        return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 2, 1, 2>(p, pl, stream)
+                         : launch_inst<BITS, META, GROUP, B, XI, 2, 0, 2>(p, pl, stream);
     }
-    if (fuse == 2) return launch_inst<BITS, META, GROUP, B, XI, 2, 2>(p, pl, stream);
-    return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 2, 1>(p, pl, stream)
-                     : launch_inst<BITS, META, GROUP, B, XI, 2, 0>(p, pl, stream);
+    if (pl.ring >= 3) {
+        if (fuse == 2) return launch_inst<BITS, META, GROUP, B, XI, 3, 2, 1>(p, pl, stream);
+        return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 3, 1, 1>(p, pl, stream)
+                         : launch_inst<BITS, META, GROUP, B, XI, 3, 0, 1>(p, pl, stream);
+    }
+    if (fuse == 2) return launch_inst<BITS, META, GROUP, B, XI, 2, 2, 1>(p, pl, stream);
+    return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 2, 1, 1>(p, pl, stream)
+                     : launch_inst<BITS, META, GROUP, B, XI, 2, 0, 1>(p, pl, stream);
 }
 
 // x items per thread: the smallest compiled count that covers the plan's.
@@ -695,17 +760,21 @@ hipError_t launch_group(const BandParams &p, const TilePlan &pl, uint32_t batch,
 }
 
 template <int BITS, int META, int GROUP>
-const void *instance_group(uint32_t batch, uint32_t xi, uint32_t ring, bool mlp) {
+const void *instance_group(uint32_t batch, uint32_t xi, uint32_t ring, bool mlp, uint32_t phases) {
     constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
+    if (mlp && phases != 1) return nullptr;
     auto pick = [&](auto bconst) -> const void * {
         constexpr int B = decltype(bconst)::value;
         auto by_ring = [&](auto xconst) -> const void * {
             constexpr int XI = decltype(xconst)::value;
+            if (phases == 2)
+                return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, 0, 2>)
+                                 : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, 0, 2>);
             if (mlp)
-                return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, 2>)
-                                 : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, 2>);
-            return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, 0>)
-                             : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, 0>);
+                return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, 2, 1>)
+                                 : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, 2, 1>);
+            return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, 0, 1>)
+                             : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, 0, 1>);
         };
         switch (xi_instance(xi)) {
             case 2: return by_ring(std::integral_constant<int, 2>{});
@@ -745,18 +814,19 @@ hipError_t launch_meta(const BandParams &p, const TilePlan &pl, uint32_t group, 
 }
 
 template <int BITS, int META>
-const void *instance_meta(uint32_t group, uint32_t batch, uint32_t xi, uint32_t ring, bool mlp) {
+const void *instance_meta(uint32_t group, uint32_t batch, uint32_t xi, uint32_t ring, bool mlp, uint32_t phases) {
     switch (group) {
-        case 32: return instance_group<BITS, META, 32>(batch, xi, ring, mlp);
-        case 64: return instance_group<BITS, META, 64>(batch, xi, ring, mlp);
-        case 128: return instance_group<BITS, META, 128>(batch, xi, ring, mlp);
+        case 32: return instance_group<BITS, META, 32>(batch, xi, ring, mlp, phases);
+        case 64: return instance_group<BITS, META, 64>(batch, xi, ring, mlp, phases);
+        case 128: return instance_group<BITS, META, 128>(batch, xi, ring, mlp, phases);
         default: return nullptr;
     }
 }
 
 template hipError_t launch_meta<QMR_BAND_BITS, QMR_BAND_META>(const BandParams &, const TilePlan &, uint32_t, uint32_t,
                                                                hipStream_t);
-template const void *instance_meta<QMR_BAND_BITS, QMR_BAND_META>(uint32_t, uint32_t, uint32_t, uint32_t, bool);
+template const void *instance_meta<QMR_BAND_BITS, QMR_BAND_META>(uint32_t, uint32_t, uint32_t, uint32_t, bool,
+                                                                   uint32_t);
 
 }  // namespace band
 
@@ -800,17 +870,17 @@ uint32_t log2_exact(uint32_t v) {
     return k;
 }
 
-const void *instance(const AffineArgs &a, uint32_t xi, uint32_t ring) {
+const void *instance(const AffineArgs &a, uint32_t xi, uint32_t ring, uint32_t phases = 1) {
     const int meta = static_cast<int>(a.meta);
     const bool mlp = a.up_w != nullptr;
     if (a.bits == 4) {
-        if (meta == 0) return instance_meta<4, 0>(a.group, a.batch, xi, ring, mlp);
-        if (meta == 1) return instance_meta<4, 1>(a.group, a.batch, xi, ring, mlp);
-        return instance_meta<4, 2>(a.group, a.batch, xi, ring, mlp);
+        if (meta == 0) return instance_meta<4, 0>(a.group, a.batch, xi, ring, mlp, phases);
+        if (meta == 1) return instance_meta<4, 1>(a.group, a.batch, xi, ring, mlp, phases);
+        return instance_meta<4, 2>(a.group, a.batch, xi, ring, mlp, phases);
     }
-    if (meta == 0) return instance_meta<8, 0>(a.group, a.batch, xi, ring, mlp);
-    if (meta == 1) return instance_meta<8, 1>(a.group, a.batch, xi, ring, mlp);
-    return instance_meta<8, 2>(a.group, a.batch, xi, ring, mlp);
+    if (meta == 0) return instance_meta<8, 0>(a.group, a.batch, xi, ring, mlp, phases);
+    if (meta == 1) return instance_meta<8, 1>(a.group, a.batch, xi, ring, mlp, phases);
+    return instance_meta<8, 2>(a.group, a.batch, xi, ring, mlp, phases);
 }
 
 // Resident workgroups per CU for an instance, block size and dynamic LDS,
@@ -852,7 +922,7 @@ bool affine_tile_supported(const AffineArgs &a) {
 }
 
 TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_kw, uint32_t force_tr,
-                          uint32_t force_ns, uint32_t force_ring) {
+                          uint32_t force_ns, uint32_t force_ring, uint32_t force_phases) {
     TilePlan pl;
     if (!affine_tile_supported(a)) return pl;
     const uint32_t row_tiles = (a.rows + 15) / 16;
@@ -991,8 +1061,40 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     // entries per wave) keep their plans.
     if (pl.kw > 0 && !mlp && (a.batch == 1 || a.bits == 8) && pl.tr >= 4 && !force_kw && !force_tr && !force_ns &&
         !force_ring && pl.n_entries < 8 * pl.ns * pl.kw) {
-        const TilePlan half = plan_affine_tile(a, lim, pl.kw, pl.tr / 2, pl.ns, pl.ring);
+        const TilePlan half = plan_affine_tile(a, lim, pl.kw, pl.tr / 2, pl.ns, pl.ring, force_phases);
         if (half.kw > 0) pl = half;
+    }
+    // Two-phase x staging for single-split plans of one wave per tile that
+    // take several rounds of workgroups (matrices too tall for one round):
+    // half the x images in LDS lets more workgroups share a CU, so one
+    // workgroup's x conversion overlaps another's stream. Taken when it
+    // raises the resident workgroups per CU: at 151936x5120 Q4/g64 (8-tile
+    // bands, 1187 workgroups) B=2 and B=3 go from one workgroup per CU to
+    // two, measured on MI355X at 92 -> 83 us (B=2) and 95.5 -> 88.8 us (B=3),
+    // three alternating runs each. Where residency stays the same the
+    // phase switch only costs (B=1 there: 71.7 -> 75.9 us forced), and at
+    // B=4 the halved images still leave one workgroup per CU.
+    if (pl.kw == 1 && !mlp && pl.ns == 1 && force_phases != 1 && pl.n_entries >= 4) {
+        const uint32_t threads = pl.tr * 64;
+        // The second phase starts at a whole pass of the ring.
+        const uint32_t pe = std::max(pl.ring, pl.n_entries / 2 / pl.ring * pl.ring);
+        const uint32_t nt1 = std::min(pe * tpe, tiles);
+        const uint32_t cap = std::max(nt1, tiles - nt1);
+        const uint32_t xi2 = (cap * a.batch * 16 + threads - 1) / threads;
+        const size_t img2 = size_t(cap) * timg;
+        const size_t lds2 = size_t(pl.meta_bytes) + img2 + size_t(pl.tr) * a.batch * 16 * 4;
+        if (xi2 <= 8 && lds2 <= lim.max_lds_per_block) {
+            const uint32_t r1 = resident_per_cu(instance(a, pl.xi, pl.ring), threads, pl.lds);
+            const uint32_t r2 = resident_per_cu(instance(a, xi2, pl.ring, 2), threads, lds2);
+            const bool rounds = double(pl.nbands) > double(r1) * cus;
+            if (force_phases == 2 || (rounds && r2 > r1)) {
+                pl.phases = 2;
+                pl.phase_entry = pe;
+                pl.xi = xi2;
+                pl.img_bytes = uint32_t(img2);
+                pl.lds = lds2;
+            }
+        }
     }
     return pl;
 }
@@ -1048,6 +1150,10 @@ hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned 
     for (uint32_t k = 0; k < 5; ++k) p.split_e[k] = host_split_begin(k, pl.ns, pl.n_entries);
     p.kw_shift = log2_exact(pl.kw);
     p.unit_shift = meta_unit_shift(a, pl.ns, pl.n_entries);
+    p.phase_entry = pl.phases == 2 ? pl.phase_entry : pl.n_entries;
+    p.phase_tiles = std::min(p.phase_entry * (8u / a.bits), pl.tiles);
+    if (pl.phases == 2 && (pl.phase_entry == 0 || pl.phase_entry >= pl.n_entries || pl.phase_entry % pl.ring != 0))
+        return hipErrorInvalidValue;
     const int meta = static_cast<int>(a.meta);
     if (a.bits == 4) {
         if (meta == 0) return launch_meta<4, 0>(p, pl, a.group, a.batch, stream);

@@ -205,11 +205,15 @@ struct TilePlan {
     uint32_t ring = 0;        // code entries in flight per wave (2 or 3)
     size_t lds = 0;           // dynamic LDS bytes per workgroup
     bool elect = false;       // every split publishes; an arrival counter elects each band's finisher
+    uint32_t phases = 1;      // 2: x images staged in two halves (single split, one wave per tile)
+    uint32_t phase_entry = 0; // with phases == 2: the first entry of the second half
 };
 bool affine_tile_supported(const AffineArgs &a);
-// Zeros leave the choice to the planner.
+// Zeros leave the choice to the planner; force_phases 1 keeps one phase of
+// x staging, 2 takes two where the plan allows it.
 TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t force_kw = 0,
-                          uint32_t force_tr = 0, uint32_t force_ns = 0, uint32_t force_ring = 0);
+                          uint32_t force_tr = 0, uint32_t force_ns = 0, uint32_t force_ring = 0,
+                          uint32_t force_phases = 0);
 // Workspace bytes for the partial-sum slots (0 when ns == 1).
 size_t affine_tile_workspace(const TilePlan &pl, const AffineArgs &a);
 // `partial` holds affine_tile_workspace bytes (64-bit slots: a slot counts

@@ -522,7 +522,8 @@ qmr::TilePlan forced_tile_plan(const qmr_device *dev, const qmr::AffineArgs &a,
     if (it != dev->band_plans.end()) return it->second;
     qmr::TilePlan pl = sched != BandSchedule::Legacy ? forced_tile_plan(dev, a)
                        : ks > 0 ? qmr::plan_affine_tile(a, dev->limits, uint32_t(ks % 100), uint32_t(ks / 100 % 100),
-                                                        uint32_t(ks / 10000 % 10), uint32_t(ks / 100000))
+                                                        uint32_t(ks / 10000 % 10), uint32_t(ks / 100000 % 10),
+                                                        uint32_t(ks / 1000000 % 10))
                                 : qmr::plan_affine_tile(a, dev->limits);
     if (pl.kw > 0 && sched == BandSchedule::Shared) {
         const qmr::TilePlan alt = qmr::plan_affine_tile(a, dev->limits, pl.kw, pl.tr, pl.ns, pl.ring == 3 ? 2 : 3);
@@ -546,7 +547,8 @@ hipError_t launch_band(qmr_device *dev, const qmr::AffineArgs &a, const qmr::Til
     const size_t need = qmr::affine_tile_workspace(pl, a);
     const bool elect = pl.elect && pl.ns > 1;
     dev->last_hip = "affine_band_kernel ring=" + std::to_string(pl.ring) + " ns=" + std::to_string(pl.ns) +
-                    " tr=" + std::to_string(pl.tr) + " kw=" + std::to_string(pl.kw) + (elect ? " elect" : "");
+                    " tr=" + std::to_string(pl.tr) + " kw=" + std::to_string(pl.kw) + (elect ? " elect" : "") +
+                    (pl.phases == 2 ? " phased" : "");
     qmr::TileWait wait;
     wait.status = dev->status_dev;
     wait.force_give_up = dev->force_give_up;
@@ -1507,7 +1509,7 @@ int qmr_gemv_plan(const qmr_device *device, uint32_t rows, uint32_t cols, uint32
             if (pl.kw > 0) {
                 // Row-band kernel: rr = -4, ks = ring*100000 + ns*10000 + tr*100 + kw.
                 if (rr) *rr = -4;
-                if (ks) *ks = int(pl.ring * 100000 + pl.ns * 10000 + pl.tr * 100 + pl.kw);
+                if (ks) *ks = int((pl.phases == 2 ? 2000000 : 0) + pl.ring * 100000 + pl.ns * 10000 + pl.tr * 100 + pl.kw);
                 return QMR_OK;
             }
         }

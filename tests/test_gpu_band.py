@@ -4,10 +4,11 @@ ABI, against the FP64 oracle of the reference's per-weight product
 gate (rel-L2 <= 1e-5, max-abs <= 1e-4*max|y64|).
 
 Every shape is run under plans forced through the tuning hook (rr = -4,
-ks = ring*100000 + ns*10000 + tr*100 + kw) so that each code path is taken:
+ks = phases*1000000 + ring*100000 + ns*10000 + tr*100 + kw, phases 0 for the
+planner's choice) so that each code path is taken:
 one to four K splits (the last split adds the others' epoch-tagged sums),
 one to eight row tiles per band, one to eight waves per tile, two- and
-three-entry rings; row tails, K tails that end inside a tile or inside a
+three-entry rings, x staged in one or two phases; row tails, K tails that end inside a tile or inside a
 128-byte entry, Q8, groups 32/64/128, F32/BF16/F16 metadata, and metadata
 runs that are not 16-byte multiples (per-value staging path).
 """
@@ -226,3 +227,60 @@ def test_elected_finishers_residual_form_in_place(gpu):
     assert kernel.endswith(" elect"), kernel
     want = oracle.matmul_f64(*m, "bf16", x, rows, cols, 4, 64, batch, 16) + r.astype(np.float64)
     assert_gate(gpu.read_f32(rb, batch * rows), want, "elected residual in place")
+
+
+PHASED_CASES = [
+    # rows, cols, bits, group, batch, kind, ring, tr
+    (40960, 2048, 4, 64, 2, "bf16", 2, 8),    # 8 entries: the second half starts at entry 4
+    (70000, 1152, 8, 64, 3, "f32", 3, 8),     # Q8 (one tile per entry), a row tail
+    (300, 4160, 4, 64, 2, "f32", 3, 4),       # 17 entries, K ends inside a tile and an entry
+    (1000, 5120, 8, 64, 1, "f16", 2, 2),      # Q8, F16 metadata, 40 entries
+    (72, 2048, 4, 128, 4, "bf16", 3, 2),      # group 128, four RHS, 4.5 row tiles
+    (260, 576, 4, 64, 1, "bf16", 2, 8),       # 3 entries: too short for two phases, one phase runs
+    (24, 4096, 8, 32, 2, "bf16", 2, 2),       # group 32, fewer rows than two tiles
+]
+
+
+@pytest.mark.parametrize("rows,cols,bits,group,batch,kind,ring,tr", PHASED_CASES)
+def test_two_phase_x_staging(gpu, rows, cols, bits, group, batch, kind, ring, tr):
+    """Single-split plans of one wave per tile forced to stage x in two
+    phases (ks + 2000000): the K tiles of the first half of the entries are
+    staged, streamed, then replaced by those of the second half in the same
+    LDS. Against the FP64 oracle, and bit-identical to the same plan with
+    one phase (ks + 1000000): each tile's product and the order of the sums
+    are the same."""
+    rng = np.random.default_rng([rows, cols, bits, group, batch, 77])
+    m = _matrix(rng, rows, cols, bits, group, kind)
+    x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
+    want = oracle.matmul_f64(*m, kind, x, rows, cols, bits, group, batch, 16)
+    ks = _ks(ring, 1, tr, 1)
+    print(f"two-phase {rows}x{cols} Q{bits}/g{group} {kind} B={batch} ring {ring} tr {tr}", flush=True)
+    got, kernel = _run(gpu, m, x, rows, cols, bits, group, batch, kind, (-4, 2000000 + ks))
+    label = f"affine_band_kernel ring={ring} ns=1 tr={tr} kw=1"
+    entries = -(-cols * bits // 8 // 128)
+    assert kernel == (label + " phased" if entries >= 4 else label), kernel
+    assert_gate(got, want, f"two-phase {rows}x{cols} ({kernel})")
+    one, kernel1 = _run(gpu, m, x, rows, cols, bits, group, batch, kind, (-4, 1000000 + ks))
+    assert kernel1 == label, kernel1
+    assert np.array_equal(got.view(np.uint32), one.view(np.uint32)), "two phases differ from one"
+
+
+@pytest.mark.parametrize("in_place", [False, True])
+def test_two_phase_x_staging_residual_form(gpu, in_place):
+    rng = np.random.default_rng([43, int(in_place)])
+    rows, cols, batch = 17408, 5120, 3
+    m = _matrix(rng, rows, cols, 4, 64, "bf16")
+    x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
+    r = rng.normal(0, 1, batch * rows).astype(np.float32)
+    bufs = [gpu.upload_bytes(np.ascontiguousarray(a)) for a in m] + [gpu.upload_f32(x.ravel())]
+    rb = gpu.upload_f32(r)
+    yb = rb if in_place else gpu.alloc_f32(batch * rows)
+    gpu.set_gemv_plan(-4, 2000000 + _ks(3, 1, 8, 1))
+    try:
+        gpu.dispatch("matmul_affine_add_bf16", bufs + [rb, yb], [rows, cols, 4, 64, batch])
+        kernel = gpu.last_hip_kernel()
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    assert kernel == "affine_band_kernel ring=3 ns=1 tr=8 kw=1 phased", kernel
+    want = oracle.matmul_f64(*m, "bf16", x, rows, cols, 4, 64, batch, 16) + r.astype(np.float64)
+    assert_gate(gpu.read_f32(yb, batch * rows), want, f"two-phase residual in_place={in_place}")
