@@ -63,6 +63,7 @@ namespace qmr {
 namespace band {
 
 constexpr int kMaxThreads = 512;  // up to 8 waves: x staging needs up to 8 items of registers per thread
+constexpr uint32_t kBandSplits = 4;  // most K splits of a band
 
 struct BandParams {
     const uint32_t *w;
@@ -94,7 +95,7 @@ struct BandParams {
     uint32_t gp;          // LDS pitch of a row's staged metadata (odd)
     uint32_t meta_bytes;  // LDS bytes of the staged metadata (16-byte multiple)
     uint32_t img_bytes;   // LDS bytes of the staged x images
-    uint32_t split_e[5];  // first entry of each split, then n_entries (host_split_begin)
+    uint32_t split_e[kBandSplits + 1];  // first entry of each split, then n_entries (host_split_begin)
     uint32_t kw_shift;    // log2(kw)
     uint32_t unit_shift;  // log2 of the threads per row in the metadata loads (>= units per row)
     // Two-phase x staging (single-split plans with one wave per tile): the
@@ -123,6 +124,7 @@ namespace {
 
 using namespace mfma;
 using band::BandParams;
+using band::kBandSplits;
 using band::kMaxThreads;
 
 constexpr int kMetaUnits = 4;  // 16-byte metadata loads per thread and plane (fast path)
@@ -581,19 +583,24 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     // past the host's spin limit it gives up: the caller writes NaN and
     // reports the band in the status word, which the host turns into a
     // failed command at its finish.
-    auto take_at = [&](unsigned long long *q, bool &ok) -> float {
-        unsigned long long word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The finisher requests every slot it needs at once (one round trip
+    // where the other splits have all published: `fetch`), then polls only
+    // the words that lack the launch's epoch (`settle`).
+    auto fetch = [&](unsigned long long *q) -> unsigned long long {
+        return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto settle = [&](unsigned long long word, unsigned long long *q, bool &ok) -> float {
         for (uint32_t spin = 0; uint32_t(word >> 32) != p.wait_epoch; ++spin) {
             if (spin >= p.spin_limit) {
                 ok = false;
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
-            word = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            word = fetch(q);
         }
         return __uint_as_float(uint32_t(word));
     };
-    auto take = [&](uint32_t k, bool &ok) -> float { return take_at(p.partial + size_t(k) * stride + oy, ok); };
+    auto slot = [&](uint32_t k) { return p.partial + size_t(k) * stride + oy; };
     auto report = [&](bool ok) {
         if (!ok && p.status) __hip_atomic_store(p.status, 0x80000000u | band, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     };
@@ -601,7 +608,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         const unsigned long long word = (static_cast<unsigned long long>(p.epoch) << 32) | __float_as_uint(value);
         __hip_atomic_store(q, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
-    auto publish = [&](uint32_t k, float value) { publish_at(p.partial + size_t(k) * stride + oy, value); };
+    auto publish = [&](uint32_t k, float value) { publish_at(slot(k), value); };
     // The election, after this workgroup's slots are published (every
     // thread calls it): whether this workgroup finishes the band. The counter
     // only elects; a finisher takes each slot once it carries the launch's
@@ -646,12 +653,24 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         bool ok = true;
         float g = v, u = vu;
         if (p.ns > 1) {
-            float sg = split == 0 ? v : take(0, ok), su = split == 0 ? vu : take(1, ok);
-            float sx = split == 0 ? ss : take_at(sq_slot(0), ok);
-            for (uint32_t k = 1; k < p.ns; ++k) {
-                sg += k == split ? v : take(2 * k, ok);
-                su += k == split ? vu : take(2 * k + 1, ok);
-                sx += k == split ? ss : take_at(sq_slot(k), ok);
+            unsigned long long wg[kBandSplits], wu[kBandSplits], wx[kBandSplits];
+#pragma unroll
+            for (uint32_t k = 0; k < kBandSplits; ++k) {
+                const bool other = k < p.ns && k != split;
+                wg[k] = other ? fetch(slot(2 * k)) : 0ull;
+                wu[k] = other ? fetch(slot(2 * k + 1)) : 0ull;
+                wx[k] = other ? fetch(sq_slot(k)) : 0ull;
+            }
+            float sg = 0.f, su = 0.f, sx = 0.f;
+#pragma unroll
+            for (uint32_t k = 0; k < kBandSplits; ++k) {
+                if (k >= p.ns) break;
+                const float kg = k == split ? v : settle(wg[k], slot(2 * k), ok);
+                const float ku = k == split ? vu : settle(wu[k], slot(2 * k + 1), ok);
+                const float kx = k == split ? ss : settle(wx[k], sq_slot(k), ok);
+                sg = k == 0 ? kg : sg + kg;
+                su = k == 0 ? ku : su + ku;
+                sx = k == 0 ? kx : sx + kx;
             }
             g = sg;
             u = su;
@@ -678,12 +697,19 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
             // published), leaving the workspace zero for the next launch
             // (which may then reuse the same epoch).
             bool ok = true;
-            float sum = split == 0 ? v : take(0, ok);
-            for (uint32_t k = 1; k < p.ns; ++k) sum += k == split ? v : take(k, ok);
+            unsigned long long w[kBandSplits];
+#pragma unroll
+            for (uint32_t k = 0; k < kBandSplits; ++k) w[k] = k < p.ns && k != split ? fetch(slot(k)) : 0ull;
+            float sum = 0.f;
+#pragma unroll
+            for (uint32_t k = 0; k < kBandSplits; ++k) {
+                if (k >= p.ns) break;
+                const float kv = k == split ? v : settle(w[k], slot(k), ok);
+                sum = k == 0 ? kv : sum + kv;
+            }
             if (p.reset_slots)
                 for (uint32_t k = 0; k < nsets; ++k)
-                    __hip_atomic_store(p.partial + size_t(k) * stride + oy, 0ull, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(slot(k), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             y = ok ? sum : __builtin_nanf("");
             report(ok);
         }
@@ -976,7 +1002,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
         if (pass == 1 && mlp && !force_ns) break;
         for (uint32_t ring : {2u, 3u}) {
             if (force_ring && ring != force_ring) continue;
-            for (uint32_t ns = 1; ns <= 4; ++ns) {
+            for (uint32_t ns = 1; ns <= band::kBandSplits; ++ns) {
                 if (force_ns && ns != force_ns) continue;
                 if (pass == 1 && ns != 1 && !force_ns) continue;
                 if (ns > n_entries) continue;
@@ -1147,7 +1173,7 @@ hipError_t launch_affine_tile(const AffineArgs &a, const TilePlan &pl, unsigned 
     p.gp = pl.gp;
     p.meta_bytes = pl.meta_bytes;
     p.img_bytes = pl.img_bytes;
-    for (uint32_t k = 0; k < 5; ++k) p.split_e[k] = host_split_begin(k, pl.ns, pl.n_entries);
+    for (uint32_t k = 0; k <= band::kBandSplits; ++k) p.split_e[k] = host_split_begin(k, pl.ns, pl.n_entries);
     p.kw_shift = log2_exact(pl.kw);
     p.unit_shift = meta_unit_shift(a, pl.ns, pl.n_entries);
     p.phase_entry = pl.phases == 2 ? pl.phase_entry : pl.n_entries;
