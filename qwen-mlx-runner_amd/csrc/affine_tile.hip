@@ -142,7 +142,7 @@ constexpr int kMetaUnits = 4;  // 16-byte metadata loads per thread and plane (f
 template <int BITS, int META, int GROUP, int B, int XI, int P, int FUSE, int PH>
 __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) {
     constexpr bool MLP = FUSE == 2;
-    static_assert(PH == 1 || (PH == 2 && !MLP), "two-phase staging serves the plain and residual forms");
+    static_assert(PH == 1 || PH == 2, "one or two phases of x staging");
     constexpr int NGM = kTileK / GROUP;  // quant groups per tile
     constexpr int SLOTS = 16 / NGM;      // A rows per quant group
     constexpr int HALF = SLOTS / 2;      // RHS per quant group in D (>= B)
@@ -205,10 +205,11 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.s), 0, int(p.m_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t br =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.b), 0, int(p.m_bytes), kRsrcWord3);
-    // The MLP form's up-matrix metadata. A staged row's loads go to both
-    // matrices, the other matrix's through kOut (zeros), and are OR-ed: the
-    // row's matrix differs between lanes, and a per-lane buffer resource
-    // would put every load in a readfirstlane loop.
+    // The MLP form's up-matrix metadata. The 16-byte unit loads read one
+    // matrix per unit; the per-value path (rows whose runs are not 16-byte
+    // multiples) loads from both, the other matrix's through kOut (zeros),
+    // and ORs them: there the row's matrix differs between lanes, and a
+    // per-lane buffer resource would put every load in a readfirstlane loop.
     const __amdgpu_buffer_rsrc_t sr2 = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void *>(MLP ? p.s2 : p.s), 0, int(p.m_bytes), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t br2 = __builtin_amdgcn_make_buffer_rsrc(
@@ -268,25 +269,34 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     // mat_rows are the up matrix's rows rl - mat_rows).
     auto mrow = [&](uint32_t rl) -> uint32_t { return band_row0 + (MLP && rl >= mat_rows ? rl - mat_rows : rl); };
     auto unit_off = [&](uint32_t rl) -> uint32_t { return (mrow(rl) * nG + Ga) * MB + ucol * 16u; };
-    auto load_units = [&](uint32_t rl, uint32_t off, u4 &sv, u4 &bv) {
-        if constexpr (MLP) {
-            const bool up_row = rl >= mat_rows;
-            const uint32_t og = up_row ? kOut : off, ou = up_row ? off : kOut;
-            sv = __builtin_amdgcn_raw_buffer_load_b128(sr, int(og), 0, 0) |
-                 __builtin_amdgcn_raw_buffer_load_b128(sr2, int(ou), 0, 0);
-            bv = __builtin_amdgcn_raw_buffer_load_b128(br, int(og), 0, 0) |
-                 __builtin_amdgcn_raw_buffer_load_b128(br2, int(ou), 0, 0);
-        } else {
-            sv = __builtin_amdgcn_raw_buffer_load_b128(sr, int(off), 0, 0);
-            bv = __builtin_amdgcn_raw_buffer_load_b128(br, int(off), 0, 0);
-        }
+    // One 16-byte unit of each plane; `up` (uniform) selects the MLP form's
+    // up matrix.
+    auto load_units = [&](bool up, uint32_t off, u4 &sv, u4 &bv) {
+        sv = __builtin_amdgcn_raw_buffer_load_b128(up ? sr2 : sr, int(off), 0, 0);
+        bv = __builtin_amdgcn_raw_buffer_load_b128(up ? br2 : br, int(off), 0, 0);
+    };
+    // Unrolled unit u's staged row: urow + u*rstep; in the MLP form the first
+    // half of the units take gate rows urow + u*rstep and the second half the
+    // up matrix's same rows (staged mat_rows further), so that every load
+    // reads one matrix through a uniform resource.
+    constexpr int kHalfUnits = kMetaUnits / 2;
+    auto unit_row = [&](int u) -> uint32_t {
+        if constexpr (MLP)
+            return (u < kHalfUnits ? 0u : mat_rows) + urow + uint32_t(u % kHalfUnits) * rstep;
+        else
+            return urow + uint32_t(u) * rstep;
+    };
+    auto unit_live = [&](int u) -> bool {
+        if constexpr (MLP)
+            return urow + uint32_t(u % kHalfUnits) * rstep < mat_rows;
+        else
+            return urow + uint32_t(u) * rstep < band_rows;
     };
     u4 ms[kMetaUnits], mbv[kMetaUnits];
 #pragma unroll
     for (int u = 0; u < kMetaUnits; ++u) {
-        const uint32_t rl = urow + uint32_t(u) * rstep;
-        const uint32_t off = (ucol_ok && rl < band_rows) ? unit_off(rl) : kOut;
-        load_units(rl, off, ms[u], mbv[u]);
+        const uint32_t off = (ucol_ok && unit_live(u)) ? unit_off(unit_row(u)) : kOut;
+        load_units(MLP && u >= kHalfUnits, off, ms[u], mbv[u]);
     }
 
     // ---- 3. The first P entries of codes. An entry is 128 contiguous bytes
@@ -351,15 +361,18 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         }
         stage_x_item<BITS, GROUP, B>(xv[i], it, it < items, lane, imgA, imgS);
     }
-    if constexpr (MLP) {
+    // Each wave's sums of squares to LDS (with two phases, once the second
+    // phase's items are added).
+    auto put_sq = [&]() {
 #pragma unroll
-        for (int t = 0; t < B; ++t) {
+        for (int t = 0; t < (MLP ? B : 1); ++t) {
             float v = xsq[t];
 #pragma unroll
             for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
             if (lane == 0) sq[wave * B + t] = v;
         }
-    }
+    };
+    if constexpr (MLP && PH == 1) put_sq();
     // ---- 5. Metadata to LDS. ----
     if (vec_meta) {
         // This thread's units hold groups g .. g+VEC-1 of their rows (g
@@ -390,15 +403,23 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         };
         if (ucol_ok) {
 #pragma unroll
-            for (int u = 0; u < kMetaUnits; ++u) {
-                const uint32_t rl = urow + uint32_t(u) * rstep;
-                if (rl < band_rows) put(rl, ms[u], mbv[u]);
-            }
+            for (int u = 0; u < kMetaUnits; ++u)
+                if (unit_live(u)) put(unit_row(u), ms[u], mbv[u]);
             // Bands with more rows than the unrolled loads cover read the rest here.
-            for (uint32_t rl = urow + uint32_t(kMetaUnits) * rstep; rl < band_rows; rl += rstep) {
-                u4 sv, bv;
-                load_units(rl, unit_off(rl), sv, bv);
-                put(rl, sv, bv);
+            if constexpr (MLP) {
+                for (uint32_t rl = urow + uint32_t(kHalfUnits) * rstep; rl < mat_rows; rl += rstep) {
+                    u4 sv, bv;
+                    load_units(false, unit_off(rl), sv, bv);
+                    put(rl, sv, bv);
+                    load_units(true, unit_off(rl + mat_rows), sv, bv);
+                    put(rl + mat_rows, sv, bv);
+                }
+            } else {
+                for (uint32_t rl = urow + uint32_t(kMetaUnits) * rstep; rl < band_rows; rl += rstep) {
+                    u4 sv, bv;
+                    load_units(false, unit_off(rl), sv, bv);
+                    put(rl, sv, bv);
+                }
             }
         }
     } else {
@@ -517,12 +538,22 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         uint32_t base = 0;
         for (; base + P < pe; base += P) pass(base);
         const uint32_t items2 = (nT - nT1) * B * 16u;
+        const uint32_t col2 = (ST0 + nT1) * kTileK;
         float x2[XI][8];
+        [[maybe_unused]] float nv2[MLP ? XI : 1][8];
 #pragma unroll
         for (int i2 = 0; i2 < XI; ++i2) {
             const uint32_t it = uint32_t(tid) + uint32_t(i2 * nthr);
-            load_x8(x2[i2], xr, uint32_t(item_pos<B>(it).t), (ST0 + nT1) * kTileK + item_col<B>(it), p.cols,
-                    it < items2);
+            load_x8(x2[i2], xr, uint32_t(item_pos<B>(it).t), col2 + item_col<B>(it), p.cols, it < items2);
+        }
+        if constexpr (MLP) {
+            const __amdgpu_buffer_rsrc_t nr =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p.norm), 0, int(p.cols * 4u), kRsrcWord3);
+#pragma unroll
+            for (int i2 = 0; i2 < XI; ++i2) {
+                const uint32_t it = uint32_t(tid) + uint32_t(i2 * nthr);
+                load_x8(nv2[i2], nr, 0u, col2 + item_col<B>(it), p.cols, it < items2);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         pass(base);
@@ -531,8 +562,19 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         for (int i2 = 0; i2 < XI; ++i2) {
             const uint32_t it = uint32_t(tid) + uint32_t(i2 * nthr);
             if (i2 > 0 && uint32_t(tid) - uint32_t(lane) + uint32_t(i2 * nthr) >= items2) break;
+            if constexpr (MLP) {
+                float q = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) q += x2[i2][j] * x2[i2][j];
+                const uint32_t it_t = item_pos<B>(it).t;
+#pragma unroll
+                for (int t = 0; t < B; ++t) xsq[t] += it_t == uint32_t(t) ? q : 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x2[i2][j] *= nv2[i2][j];
+            }
             stage_x_item<BITS, GROUP, B>(x2[i2], it, it < items2, lane, imgA, imgS);
         }
+        if constexpr (MLP) put_sq();
         stage_x_pads<GROUP, B>(nT - nT1, tid, nthr, imgS);
         lds_barrier();
         img_base = nT1;
@@ -733,10 +775,13 @@ hipError_t launch_xi(const BandParams &p, const TilePlan &pl, hipStream_t stream
     const int fuse = p.w2 != nullptr ? 2 : p.r != nullptr ? 1 : 0;
     if (pl.phases == 2) {
         // Every wave must stream the same entries to meet the phase barriers.
-        if (fuse == 2 || pl.ns != 1 || pl.kw != 1) return hipErrorInvalidValue;
-        if (pl.ring >= 3)
+        if (pl.ns != 1 || pl.kw != 1) return hipErrorInvalidValue;
+        if (pl.ring >= 3) {
+            if (fuse == 2) return launch_inst<BITS, META, GROUP, B, XI, 3, 2, 2>(p, pl, stream);
             return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 3, 1, 2>(p, pl, stream)
                              : launch_inst<BITS, META, GROUP, B, XI, 3, 0, 2>(p, pl, stream);
+        }
+        if (fuse == 2) return launch_inst<BITS, META, GROUP, B, XI, 2, 2, 2>(p, pl, stream);
         return fuse == 1 ? launch_inst<BITS, META, GROUP, B, XI, 2, 1, 2>(p, pl, stream)
                          : launch_inst<BITS, META, GROUP, B, XI, 2, 0, 2>(p, pl, stream);
     }
@@ -788,11 +833,13 @@ hipError_t launch_group(const BandParams &p, const TilePlan &pl, uint32_t batch,
 template <int BITS, int META, int GROUP>
 const void *instance_group(uint32_t batch, uint32_t xi, uint32_t ring, bool mlp, uint32_t phases) {
     constexpr int MAXB = (16 / (kTileK / GROUP)) / 2;
-    if (mlp && phases != 1) return nullptr;
     auto pick = [&](auto bconst) -> const void * {
         constexpr int B = decltype(bconst)::value;
         auto by_ring = [&](auto xconst) -> const void * {
             constexpr int XI = decltype(xconst)::value;
+            if (phases == 2 && mlp)
+                return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, 2, 2>)
+                                 : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, 2, 2>);
             if (phases == 2)
                 return ring >= 3 ? reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 3, 0, 2>)
                                  : reinterpret_cast<const void *>(affine_band_kernel<BITS, META, GROUP, B, XI, 2, 0, 2>);
@@ -988,8 +1035,8 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     // pass takes single-split bands, whose workgroups never wait on each
     // other, so any number of rounds is safe: the tallest band, one wave per
     // tile, and the ring whose codes in flight per CU (resident waves x ring
-    // x 2 KB) come closest to 48 KB. The MLP form's finishers wait on other
-    // workgroups, so it has no such pass. Measured at 151936x5120 Q4/g64,
+    // x 2 KB) come closest to 48 KB. The MLP form takes this pass through
+    // the rule after it, or when forced. Measured at 151936x5120 Q4/g64,
     // two boxes: B=1 76.7-80.4 us (tr 8, kw 1, ring 2; two workgroups per
     // CU) against 86.4-89.8 for the row-owning kernel and 80.9-81.9 with
     // ring 3; B=3 95.0-96.7 (ring 3; one 106 KB workgroup per CU) against
@@ -1077,6 +1124,22 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
             }
         }
     }
+    // The MLP form where no plan fits one round (B >= 2 at the 27B gate/up
+    // shape 2 x 17408x5120): single-split bands of two gate and two up
+    // tiles with a two-entry ring, whose workgroups never wait on each
+    // other, so any number of rounds is safe (x in two phases where that
+    // raises the resident workgroups, below); where that has no plan (B=4
+    // there: more x items per thread than compiled), 8-tile bands in two
+    // splits with elected finishers. Measured on MI355X, six shuffled
+    // rounds of 200 launches, medians: B=2 28.9 us against 30.2 for the
+    // split-K kernel, B=3 30.5 against 31.3, B=4 31.8 against 32.0 (8-tile
+    // single-split bands: 31.2, 32.6 and 41.3 us; a three-entry ring at
+    // B=3: 37.3).
+    if (pl.kw == 0 && mlp && !force_kw && !force_tr && !force_ns && !force_ring) {
+        pl = plan_affine_tile(a, lim, 1, 4, 1, 2, force_phases);
+        if (pl.kw == 0) pl = plan_affine_tile(a, lim, 1, 8, 2, 2, force_phases);
+        return pl;
+    }
     // Short streams: fewer than 8 entries per wave run faster with half the
     // row tiles per band (more, shorter workgroups) where x costs little to
     // convert against the codes: at one RHS, and for 8-bit codes (twice the
@@ -1100,7 +1163,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     // three alternating runs each. Where residency stays the same the
     // phase switch only costs (B=1 there: 71.7 -> 75.9 us forced), and at
     // B=4 the halved images still leave one workgroup per CU.
-    if (pl.kw == 1 && !mlp && pl.ns == 1 && force_phases != 1 && pl.n_entries >= 4) {
+    if (pl.kw == 1 && pl.ns == 1 && force_phases != 1 && pl.n_entries >= 4) {
         const uint32_t threads = pl.tr * 64;
         // The second phase starts at a whole pass of the ring.
         const uint32_t pe = std::max(pl.ring, pl.n_entries / 2 / pl.ring * pl.ring);
@@ -1108,7 +1171,8 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
         const uint32_t cap = std::max(nt1, tiles - nt1);
         const uint32_t xi2 = (cap * a.batch * 16 + threads - 1) / threads;
         const size_t img2 = size_t(cap) * timg;
-        const size_t lds2 = size_t(pl.meta_bytes) + img2 + size_t(pl.tr) * a.batch * 16 * 4;
+        const size_t lds2 = size_t(pl.meta_bytes) + img2 + size_t(pl.tr) * a.batch * 16 * 4 +
+                            (mlp ? size_t(pl.tr) * a.batch * 4 : 0);
         if (xi2 <= 8 && lds2 <= lim.max_lds_per_block) {
             const uint32_t r1 = resident_per_cu(instance(a, pl.xi, pl.ring), threads, pl.lds);
             const uint32_t r2 = resident_per_cu(instance(a, xi2, pl.ring, 2), threads, lds2);

@@ -132,14 +132,15 @@ def test_mlp_band_form_with_elected_finishers(gpu, plan, batch):
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "launches differ"
 
 
-@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4])
 def test_mlp_default_is_the_band_kernel_at_the_27b_shape(gpu, batch):
-    """At the 27B gate/up shape and B=1 the fused form runs on the row-band
-    kernel: each band holds gate tiles and the up tiles of the same rows, so
-    one staging of x serves both matrices and the grid is one matrix's. At
-    B=3 the form's instances hold x and the norm weights together while
-    staging (175-183 VGPRs: one 512-thread workgroup per CU), no plan fits
-    one round of resident workgroups, and the split-K kernel runs it."""
+    """At the 27B gate/up shape the fused form runs on the row-band kernel:
+    each band holds gate tiles and the up tiles of the same rows, so one
+    staging of x serves both matrices and the grid is one matrix's. At B=1
+    a plan fits one round of resident workgroups; at B=2 and B=3 none does,
+    and single-split bands of two gate and two up tiles run over several
+    rounds with x staged in two phases; at B=4, 8-tile bands in two splits
+    with elected finishers."""
     rows, cols = 17408, 5120
     rng = np.random.default_rng(batch)
     gate_m = _matrix(rng, rows, cols, 4, 64, "bf16")
@@ -148,8 +149,40 @@ def test_mlp_default_is_the_band_kernel_at_the_27b_shape(gpu, batch):
     nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
     _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, 4, 64, batch, "bf16")
     kernel = gpu.last_hip_kernel()
-    want = "affine_band_kernel" if batch == 1 else "affine_mfma_kernel"
-    assert kernel.startswith(want) and kernel.endswith("(MLP)"), kernel
+    want = {1: "affine_band_kernel ring=2 ns=1 tr=4 kw=1 (MLP)",
+            2: "affine_band_kernel ring=2 ns=1 tr=4 kw=1 phased (MLP)",
+            3: "affine_band_kernel ring=2 ns=1 tr=4 kw=1 phased (MLP)",
+            4: "affine_band_kernel ring=2 ns=2 tr=8 kw=1 elect (MLP)"}[batch]
+    assert kernel == want, kernel
+
+
+@pytest.mark.parametrize("plan,batch", [(0, 2), (0, 3), (0, 4), (2210401, 2), (2310401, 3), (2210401, 1)])
+def test_mlp_band_form_single_split_over_several_rounds(gpu, plan, batch):
+    """The row-band MLP form at the 27B gate/up shape with single-split
+    bands over several rounds of workgroups (the default at B=2..4, and
+    forced plans with x staged in two phases: the norm weights and the sums
+    of squares of the second half's columns are taken when that half is
+    staged). Against the FP64 oracle and deterministic."""
+    rows, cols = 17408, 5120
+    rng = np.random.default_rng(plan + batch + 3)
+    gate_m = _matrix(rng, rows, cols, 4, 64, "bf16")
+    up_m = _matrix(rng, rows, cols, 4, 64, "bf16")
+    x = rng.standard_normal((batch, cols)).astype(np.float32) * 3
+    nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    want = oracle.mlp_gate_up_f64(gate_m, up_m, "bf16", x, nw, EPS, rows, cols, 4, 64, batch, 16)
+    print(f"mlp single-split plan {plan} B={batch}", flush=True)
+    gpu.set_gemv_plan(-4 if plan else 0, plan)
+    try:
+        got = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, 4, 64, batch, "bf16")
+        kernel = gpu.last_hip_kernel()
+        again = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, 4, 64, batch, "bf16")
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    assert kernel.startswith("affine_band_kernel") and kernel.endswith("(MLP)"), kernel
+    if plan:
+        assert kernel.endswith(" ns=1 tr=4 kw=1 phased (MLP)"), kernel
+    assert_gate(got, want, f"mlp single-split {plan} B{batch} ({kernel})")
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "launches differ"
 
 
 def test_mlp_rms_statistic_covers_every_column_and_rhs(gpu):
