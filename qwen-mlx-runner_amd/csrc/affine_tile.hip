@@ -725,6 +725,13 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         return;
     } else {
         float y = v;
+        // The residual form's r, requested before the cross-split sum so that
+        // its round trip overlaps the slot reads (with elected finishers
+        // every split requests it; the one elected uses it). In place (y is
+        // r) each element is read and then written by the same thread.
+        [[maybe_unused]] float rv = 0.f;
+        if constexpr (FUSE == 1)
+            if (live && (elect || split + 1 == p.ns)) rv = p.r[oy];
         if (p.ns > 1) {
             if (elect) {
                 if (live) publish(split, v);
@@ -755,7 +762,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
             y = ok ? sum : __builtin_nanf("");
             report(ok);
         }
-        p.y[oy] = FUSE == 1 ? p.r[oy] + y : y;
+        p.y[oy] = FUSE == 1 ? rv + y : y;
     }
 }
 
