@@ -241,10 +241,13 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
  *            the row-slot tiling).
  *   rr > 0 with ks > 0: the vector-ALU row-slot kernel with `rr` rows per
  *            slot and a K-split of `ks`.
- *   rr = -4: row-band matrix-core kernel; ks = ring*100000 + ns*10000 +
- *            tr*100 + kw pins its ring depth (2 or 3), K splits, row tiles
- *            per band (the MLP form: tr/2 gate and tr/2 up tiles) and waves
- *            per tile; zero fields and ks = 0 leave them to its planner.
+ *   rr = -4: row-band matrix-core kernel; ks = phases*1000000 +
+ *            ring*100000 + ns*10000 + tr*100 + kw pins its x staging
+ *            phases (1, or 2 for single-split plans of one wave per tile),
+ *            ring depth (2 or 3), K splits (1-8; its planner takes at most
+ *            4), row tiles per band (the MLP form: tr/2 gate and tr/2 up
+ *            tiles) and waves per tile; zero fields and ks = 0 leave them
+ *            to its planner.
  *   rr = -5: dense F16 products (matvec_f16, matmul_f16) on the matrix-core
  *            kernel with ks = ring*10000 + kw*1000 + rt*100 + ns (entries
  *            in flight per wave, 4 or 8; waves per row tile; row tiles per
@@ -258,7 +261,8 @@ int qmr_supported_bf16_quantization(uint32_t bits, size_t group);
 int qmr_set_gemv_plan(qmr_device *device, int rr, int ks);
 /* The plan the GEMV launcher uses for a shape with group 64 and BF16
  * metadata (honours a forced plan), in the encoding of qmr_set_gemv_plan;
- * the row-band kernel reports rr = -4 with its ks, the split-K kernel
+ * the row-band kernel reports rr = -4 with its ks (phases 2 as
+ * 2000000 + ..., one phase without the digit), the split-K kernel
  * rr = -2 with ks = its K splits. bits = 16: the plan of a dense F16
  * product over an aligned view (rr = -5 with its ks, or rr = -1 for the
  * vector-ALU kernels). */

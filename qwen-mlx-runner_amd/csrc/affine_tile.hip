@@ -63,7 +63,9 @@ namespace qmr {
 namespace band {
 
 constexpr int kMaxThreads = 512;  // up to 8 waves: x staging needs up to 8 items of registers per thread
-constexpr uint32_t kBandSplits = 4;  // most K splits of a band
+constexpr uint32_t kBandSplits = 8;    // most K splits of a band
+constexpr uint32_t kPlannedSplits = 4; // most the planner picks by itself (more when forced)
+constexpr uint32_t kFetchChunk = 4;    // slot words a finisher requests at once, per plane
 
 struct BandParams {
     const uint32_t *w;
@@ -125,6 +127,7 @@ namespace {
 using namespace mfma;
 using band::BandParams;
 using band::kBandSplits;
+using band::kFetchChunk;
 using band::kMaxThreads;
 
 constexpr int kMetaUnits = 4;  // 16-byte metadata loads per thread and plane (fast path)
@@ -176,9 +179,7 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     const uint32_t Gp = p.gp;
     // The split's entries (from the host: a uniform select, no division),
     // tiles, groups and columns.
-    auto split_at = [&](uint32_t k) -> uint32_t {
-        return k == 0 ? p.split_e[0] : k == 1 ? p.split_e[1] : k == 2 ? p.split_e[2] : k == 3 ? p.split_e[3] : p.split_e[4];
-    };
+    auto split_at = [&](uint32_t k) -> uint32_t { return p.split_e[k]; };
     const uint32_t SE0 = split_at(split);
     const uint32_t SE1 = split_at(split + 1);
     const uint32_t ST0 = SE0 * TPE;
@@ -625,9 +626,10 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
     // past the host's spin limit it gives up: the caller writes NaN and
     // reports the band in the status word, which the host turns into a
     // failed command at its finish.
-    // The finisher requests every slot it needs at once (one round trip
-    // where the other splits have all published: `fetch`), then polls only
-    // the words that lack the launch's epoch (`settle`).
+    // The finisher requests the slots it needs kFetchChunk splits at a time
+    // (one round trip per chunk where the other splits have all published:
+    // `fetch`), then polls only the words that lack the launch's epoch
+    // (`settle`).
     auto fetch = [&](unsigned long long *q) -> unsigned long long {
         return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
@@ -695,24 +697,28 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
         bool ok = true;
         float g = v, u = vu;
         if (p.ns > 1) {
-            unsigned long long wg[kBandSplits], wu[kBandSplits], wx[kBandSplits];
-#pragma unroll
-            for (uint32_t k = 0; k < kBandSplits; ++k) {
-                const bool other = k < p.ns && k != split;
-                wg[k] = other ? fetch(slot(2 * k)) : 0ull;
-                wu[k] = other ? fetch(slot(2 * k + 1)) : 0ull;
-                wx[k] = other ? fetch(sq_slot(k)) : 0ull;
-            }
             float sg = 0.f, su = 0.f, sx = 0.f;
+            for (uint32_t k0 = 0; k0 < p.ns; k0 += kFetchChunk) {
+                unsigned long long wg[kFetchChunk], wu[kFetchChunk], wx[kFetchChunk];
 #pragma unroll
-            for (uint32_t k = 0; k < kBandSplits; ++k) {
-                if (k >= p.ns) break;
-                const float kg = k == split ? v : settle(wg[k], slot(2 * k), ok);
-                const float ku = k == split ? vu : settle(wu[k], slot(2 * k + 1), ok);
-                const float kx = k == split ? ss : settle(wx[k], sq_slot(k), ok);
-                sg = k == 0 ? kg : sg + kg;
-                su = k == 0 ? ku : su + ku;
-                sx = k == 0 ? kx : sx + kx;
+                for (uint32_t j = 0; j < kFetchChunk; ++j) {
+                    const uint32_t k = k0 + j;
+                    const bool other = k < p.ns && k != split;
+                    wg[j] = other ? fetch(slot(2 * k)) : 0ull;
+                    wu[j] = other ? fetch(slot(2 * k + 1)) : 0ull;
+                    wx[j] = other ? fetch(sq_slot(k)) : 0ull;
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < kFetchChunk; ++j) {
+                    const uint32_t k = k0 + j;
+                    if (k >= p.ns) break;
+                    const float kg = k == split ? v : settle(wg[j], slot(2 * k), ok);
+                    const float ku = k == split ? vu : settle(wu[j], slot(2 * k + 1), ok);
+                    const float kx = k == split ? ss : settle(wx[j], sq_slot(k), ok);
+                    sg = k == 0 ? kg : sg + kg;
+                    su = k == 0 ? ku : su + ku;
+                    sx = k == 0 ? kx : sx + kx;
+                }
             }
             g = sg;
             u = su;
@@ -746,15 +752,19 @@ __global__ __launch_bounds__(kMaxThreads) void affine_band_kernel(BandParams p) 
             // published), leaving the workspace zero for the next launch
             // (which may then reuse the same epoch).
             bool ok = true;
-            unsigned long long w[kBandSplits];
-#pragma unroll
-            for (uint32_t k = 0; k < kBandSplits; ++k) w[k] = k < p.ns && k != split ? fetch(slot(k)) : 0ull;
             float sum = 0.f;
+            for (uint32_t k0 = 0; k0 < p.ns; k0 += kFetchChunk) {
+                unsigned long long w[kFetchChunk];
 #pragma unroll
-            for (uint32_t k = 0; k < kBandSplits; ++k) {
-                if (k >= p.ns) break;
-                const float kv = k == split ? v : settle(w[k], slot(k), ok);
-                sum = k == 0 ? kv : sum + kv;
+                for (uint32_t j = 0; j < kFetchChunk; ++j)
+                    w[j] = k0 + j < p.ns && k0 + j != split ? fetch(slot(k0 + j)) : 0ull;
+#pragma unroll
+                for (uint32_t j = 0; j < kFetchChunk; ++j) {
+                    const uint32_t k = k0 + j;
+                    if (k >= p.ns) break;
+                    const float kv = k == split ? v : settle(w[j], slot(k), ok);
+                    sum = k == 0 ? kv : sum + kv;
+                }
             }
             if (p.reset_slots)
                 for (uint32_t k = 0; k < nsets; ++k)
@@ -1056,7 +1066,7 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
         if (pass == 1 && mlp && !force_ns) break;
         for (uint32_t ring : {2u, 3u}) {
             if (force_ring && ring != force_ring) continue;
-            for (uint32_t ns = 1; ns <= band::kBandSplits; ++ns) {
+            for (uint32_t ns = 1; ns <= (force_ns ? band::kBandSplits : band::kPlannedSplits); ++ns) {
                 if (force_ns && ns != force_ns) continue;
                 if (pass == 1 && ns != 1 && !force_ns) continue;
                 if (ns > n_entries) continue;

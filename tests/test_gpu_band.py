@@ -6,7 +6,7 @@ gate (rel-L2 <= 1e-5, max-abs <= 1e-4*max|y64|).
 Every shape is run under plans forced through the tuning hook (rr = -4,
 ks = phases*1000000 + ring*100000 + ns*10000 + tr*100 + kw, phases 0 for the
 planner's choice) so that each code path is taken:
-one to four K splits (the last split adds the others' epoch-tagged sums),
+one to eight K splits (the last split adds the others' epoch-tagged sums),
 one to eight row tiles per band, one to eight waves per tile, two- and
 three-entry rings, x staged in one or two phases; row tails, K tails that end inside a tile or inside a
 128-byte entry, Q8, groups 32/64/128, F32/BF16/F16 metadata, and metadata
@@ -284,3 +284,26 @@ def test_two_phase_x_staging_residual_form(gpu, in_place):
     assert kernel == "affine_band_kernel ring=3 ns=1 tr=8 kw=1 phased", kernel
     want = oracle.matmul_f64(*m, "bf16", x, rows, cols, 4, 64, batch, 16) + r.astype(np.float64)
     assert_gate(gpu.read_f32(yb, batch * rows), want, f"two-phase residual in_place={in_place}")
+
+
+@pytest.mark.parametrize("rows,cols,batch,kind,plan", [
+    (5120, 17408, 3, "bf16", (3, 6, 8, 1)),   # six splits, one round
+    (5120, 17408, 1, "bf16", (2, 8, 4, 1)),   # eight splits (two chunks of slot reads)
+    (300, 4160, 2, "f32", (3, 5, 2, 2)),      # 17 entries in five splits, row and K tails
+    (17408, 5120, 3, "bf16", (2, 7, 8, 1)),   # seven splits over several rounds: elected finishers
+])
+def test_forced_plans_with_more_than_four_splits(gpu, rows, cols, batch, kind, plan):
+    """The tuning hook takes up to eight K splits (the planner itself picks
+    at most four): the finisher reads the other splits' slots four at a
+    time. Against the FP64 oracle, and deterministic."""
+    rng = np.random.default_rng([rows, cols, batch, *plan])
+    m = _matrix(rng, rows, cols, 4, 64, kind)
+    x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
+    want = oracle.matmul_f64(*m, kind, x, rows, cols, 4, 64, batch, 16)
+    print(f"many splits {rows}x{cols} B={batch} plan {plan}", flush=True)
+    got, kernel = _run(gpu, m, x, rows, cols, 4, 64, batch, kind, (-4, _ks(*plan)))
+    ring, ns, tr, kw = plan
+    assert kernel.removesuffix(" elect") == f"affine_band_kernel ring={ring} ns={ns} tr={tr} kw={kw}", kernel
+    assert_gate(got, want, f"{rows}x{cols} B={batch} plan {plan} ({kernel})")
+    again, _ = _run(gpu, m, x, rows, cols, 4, 64, batch, kind, (-4, _ks(*plan)))
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "launches differ"
