@@ -1182,24 +1182,54 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     // B=4 the halved images still leave one workgroup per CU.
     if (pl.kw == 1 && pl.ns == 1 && force_phases != 1 && pl.n_entries >= 4) {
         const uint32_t threads = pl.tr * 64;
-        // The second phase starts at a whole pass of the ring.
-        const uint32_t pe = std::max(pl.ring, pl.n_entries / 2 / pl.ring * pl.ring);
-        const uint32_t nt1 = std::min(pe * tpe, tiles);
-        const uint32_t cap = std::max(nt1, tiles - nt1);
-        const uint32_t xi2 = (cap * a.batch * 16 + threads - 1) / threads;
-        const size_t img2 = size_t(cap) * timg;
-        const size_t lds2 = size_t(pl.meta_bytes) + img2 + size_t(pl.tr) * a.batch * 16 * 4 +
-                            (mlp ? size_t(pl.tr) * a.batch * 4 : 0);
-        if (xi2 <= 8 && lds2 <= lim.max_lds_per_block) {
+        struct Phased {
+            bool ok = false;
+            uint32_t pe = 0, xi = 0, resident = 0;
+            size_t img = 0, lds = 0;
+        };
+        auto phased = [&](uint32_t ring) {
+            Phased f;
+            // The second phase starts at a whole pass of the ring.
+            f.pe = std::max(ring, pl.n_entries / 2 / ring * ring);
+            if (f.pe >= pl.n_entries) return f;
+            const uint32_t nt1 = std::min(f.pe * tpe, tiles);
+            const uint32_t cap = std::max(nt1, tiles - nt1);
+            f.xi = (cap * a.batch * 16 + threads - 1) / threads;
+            f.img = size_t(cap) * timg;
+            f.lds = size_t(pl.meta_bytes) + f.img + size_t(pl.tr) * a.batch * 16 * 4 +
+                    (mlp ? size_t(pl.tr) * a.batch * 4 : 0);
+            if (f.xi > 8 || f.lds > lim.max_lds_per_block) return f;
+            f.resident = resident_per_cu(instance(a, f.xi, ring, 2), threads, f.lds);
+            f.ok = f.resident > 0;
+            return f;
+        };
+        Phased f = phased(pl.ring);
+        if (f.ok) {
             const uint32_t r1 = resident_per_cu(instance(a, pl.xi, pl.ring), threads, pl.lds);
-            const uint32_t r2 = resident_per_cu(instance(a, xi2, pl.ring, 2), threads, lds2);
             const bool rounds = double(pl.nbands) > double(r1) * cus;
-            if (force_phases == 2 || (rounds && r2 > r1)) {
+            if (force_phases == 2 || (rounds && f.resident > r1)) {
+                // The ring is picked again for the phased residency, by the
+                // same rule as the several-round pass (codes in flight per
+                // CU closest to 48 KB). Measured on the 151936x5120 head at
+                // B=3, five shuffled rounds of 40 launches, min / median:
+                // 80.7 / 83.5 us with the two-entry ring against 82.8 / 85.8
+                // with three (B=2 level: 77.9 / 80.2 against 78.6 / 79.7).
+                if (!force_ring) {
+                    auto off = [&](uint32_t ring, const Phased &g) {
+                        return std::fabs(std::log2(double(g.resident) * pl.tr * ring * 2048.0 / 49152.0));
+                    };
+                    const uint32_t other = pl.ring == 3 ? 2 : 3;
+                    const Phased g = phased(other);
+                    if (g.ok && off(other, g) < off(pl.ring, f) - 1e-9) {
+                        pl.ring = other;
+                        f = g;
+                    }
+                }
                 pl.phases = 2;
-                pl.phase_entry = pe;
-                pl.xi = xi2;
-                pl.img_bytes = uint32_t(img2);
-                pl.lds = lds2;
+                pl.phase_entry = f.pe;
+                pl.xi = f.xi;
+                pl.img_bytes = uint32_t(f.img);
+                pl.lds = f.lds;
             }
         }
     }
