@@ -293,3 +293,35 @@ def test_fused_alias_rules_and_reference_mode(gpu):
                          params + [EPS_BITS])
     finally:
         ref.close()
+
+
+@pytest.mark.parametrize("rows,cols,bits,group,batch,kind,ring,tr", [
+    (2000, 3072, 4, 64, 2, "bf16", 2, 4),    # 12 entries: the second phase from entry 6
+    (1000, 1024, 8, 64, 1, "f16", 3, 2),     # Q8, F16 metadata, 8 entries: phases of 3 and 5
+    (300, 2048, 4, 128, 3, "f32", 2, 4),     # group 128, FP32 metadata, row tail
+    (130, 4160, 4, 64, 4, "bf16", 3, 8),     # K ends inside a tile and an entry, four RHS
+])
+def test_mlp_band_form_two_phase_staging_forced(gpu, rows, cols, bits, group, batch, kind, ring, tr):
+    """The MLP form with x staged in two phases, forced (ks = 2000000 +
+    ring*100000 + 10000 + tr*100 + 1) over formats and tails: the second
+    phase loads its columns' x and norm weights and adds their x² to each
+    RHS's statistic before the SwiGLU. Against the FP64 oracle, and
+    deterministic."""
+    rng = np.random.default_rng([rows, cols, bits, group, batch, 5])
+    gate_m = _matrix(rng, rows, cols, bits, group, kind)
+    up_m = _matrix(rng, rows, cols, bits, group, kind)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    want = oracle.mlp_gate_up_f64(gate_m, up_m, kind, x, nw, EPS, rows, cols, bits, group, batch, 8)
+    plan = 2000000 + ring * 100000 + 10000 + tr * 100 + 1
+    print(f"mlp two-phase {rows}x{cols} Q{bits}/g{group} {kind} B={batch} plan {plan}", flush=True)
+    gpu.set_gemv_plan(-4, plan)
+    try:
+        got = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind)
+        kernel = gpu.last_hip_kernel()
+        again = _run_mlp(gpu, gate_m, up_m, x, nw, rows, cols, bits, group, batch, kind)
+    finally:
+        gpu.set_gemv_plan(0, 0)
+    assert kernel == f"affine_band_kernel ring={ring} ns=1 tr={tr} kw=1 phased (MLP)", kernel
+    assert_gate(got, want, f"mlp two-phase {plan} {rows}x{cols} Q{bits}/g{group} {kind} B{batch}")
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "launches differ"
