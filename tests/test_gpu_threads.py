@@ -4,7 +4,9 @@ Each handle owns its stream, workspaces, plan caches and slot epochs; what
 the handles share (the kernels' dynamic-LDS limits, the occupancy caches of
 the planners, the GPU itself) is guarded. Each thread runs its own mix of
 launches (row-band GEMV and block with split sums, the split-K kernel forced
-to four splits, dense F16 on the matrix cores with split sums, the wide block)
+to four splits, dense F16 on the matrix cores with split sums, the wide block,
+the fused MLP form over several rounds with two-phase staging and with
+elected finishers)
 several times in its own order, and every output must equal, bit for bit,
 the same launch run alone on the session handle: a launch's sums depend only
 on its plan. ctypes releases the GIL around each C call, so the two threads'
@@ -30,6 +32,8 @@ CASES = [
     ("dense", (0, 0), (5120, 17408, 3)),
     ("dense", (-5, 408), (17408, 5120, 2)),
     ("wide", (0, 0), (2048, 5120, 64)),
+    ("mlp", (0, 0), (17408, 5120, 3)),   # band MLP form over several rounds, x in two phases
+    ("mlp", (0, 0), (17408, 5120, 4)),   # band MLP form, elected finishers
 ]
 
 
