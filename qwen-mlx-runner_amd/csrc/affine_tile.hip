@@ -1057,8 +1057,9 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
     // two boxes: B=1 76.7-80.4 us (tr 8, kw 1, ring 2; two workgroups per
     // CU) against 86.4-89.8 for the row-owning kernel and 80.9-81.9 with
     // ring 3; B=3 95.0-96.7 (ring 3; one 106 KB workgroup per CU) against
-    // 95.1-97.0 and 98.8-99.2 with ring 2. Two or three splits over several
-    // rounds measured slower at both batches.
+    // 95.1-97.0 and 98.8-99.2 with ring 2, before x was staged in two phases
+    // there (below). Two or three splits over several rounds measured slower
+    // at both batches.
     double best = 1e30;
     for (int pass = 0; pass < 2 && pl.kw == 0; ++pass) {
         // Several rounds: single-split bands; split bands with elected
