@@ -1171,6 +1171,16 @@ TilePlan plan_affine_tile(const AffineArgs &a, const DeviceLimits &lim, uint32_t
         const TilePlan half = plan_affine_tile(a, lim, pl.kw, pl.tr / 2, pl.ns, pl.ring, force_phases);
         if (half.kw > 0) pl = half;
     }
+    // Streams of at most four entries per wave take the two-entry ring: a
+    // deeper ring requests nearly the whole stream up front. Measured on
+    // MI355X, every feasible plan timed twice in shuffled order: 5120x5120
+    // Q4/g64 (3.3 entries per wave) 7.52 -> 7.18 us at B=1 and 8.20 -> 7.80
+    // at B=3; Q8 of the same shape (6.7 entries per wave) and the metric
+    // shape (11.3) keep the three-entry ring, their fastest.
+    if (pl.kw > 0 && !mlp && pl.ring == 3 && !force_ring && pl.n_entries <= 4 * pl.ns * pl.kw) {
+        const TilePlan two = plan_affine_tile(a, lim, pl.kw, pl.tr, pl.ns, 2, force_phases);
+        if (two.kw > 0) pl = two;
+    }
     // Two-phase x staging for single-split plans of one wave per tile that
     // take several rounds of workgroups (matrices too tall for one round):
     // half the x images in LDS lets more workgroups share a CU, so one

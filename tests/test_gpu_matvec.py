@@ -251,6 +251,9 @@ def test_default_plan_kernel_family(gpu, rows, cols, bits, batch, kind):
         # codes, take half-height bands; Q4 at three RHS keeps the planner's
         # own pick.
         assert plan[1] // 100 % 100 == (2 if batch == 1 or bits == 8 else 4), plan
+        # Streams of at most four entries per wave (Q4 here: 20 entries per
+        # row over three splits of two waves) take the two-entry ring.
+        assert plan[1] // 100000 % 10 == (2 if bits == 4 else 3), plan
 
 
 @pytest.mark.parametrize("rr,name,batch", [(0, "matmul_affine_bf16", 1), (0, "matmul_affine_bf16", 3),
